@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Benchmark of the Whisper-encoder hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+                    [--no-rowops] [--workload l16|l1|l16s]
+
+A step is one encoder forward (mel -> features) of the workload over inputs
+already resident in HBM, replayed as the captured hipGraph. Default workload:
+the large-v3-shaped encoder (32 layers, d 1280, 20 heads, ctx 1500) on a
+batch of 16 synthetic log-mels [16, 128, 3000]; `value` is mel-frames/s.
+The same run also reports the batch-1 latency (large-v3, ctx 1500), the
+encoder's fraction of the bf16 MFMA peak, per-stage device times (HIP events
+on the stream the kernels run on), the roofline of the dominant kernel, the
+row kernels' HBM throughput over rotating buffers larger than the 256 MB
+Infinity Cache, and the CPU baseline (the torch fp32 oracle on this host's
+cores, on a bounded sample).
+
+Prints ONE JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT / "whisper-xdna_amd"), str(ROOT)]
+
+METRIC = "large-v3 encoder ms @ctx=1500 bs=1; mel-frames/s bs=16; % bf16 MFMA peak"
+PEAK_BF16 = 2.5e15      # MI355X dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12       # MI355X HBM3E, B/s
+LARGE = dict(n_mels=128, d=1280, n_head=20, n_layer=32, n_ctx=1500)
+WORKLOADS = {
+    "l16": dict(batch=16, n_frames=3000,
+                name="whisper-large-v3-shaped encoder, batch 16, ctx 1500, 32 layers, bf16/fp32-acc"),
+    "l1": dict(batch=1, n_frames=3000,
+               name="whisper-large-v3-shaped encoder, batch 1, ctx 1500, 32 layers, bf16/fp32-acc"),
+    "l16s": dict(batch=16, n_frames=1024,
+                 name="whisper-large-v3-shaped encoder, batch 16, ctx 512, 32 layers, bf16/fp32-acc"),
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def stage_flops(g, batch, n_frames):
+    """Algorithmic FLOPs per stage of one forward (2*M*N*K per GEMM,
+    4*ctx^2*d per layer for attention; unpadded shapes)."""
+    d, nm, nl = g["d"], g["n_mels"], g["n_layer"]
+    ctx = (n_frames - 1) // 2 + 1
+    M = batch * ctx
+    return {
+        "conv1": 2 * batch * n_frames * d * 3 * nm,
+        "conv2": 2 * M * d * 3 * d,
+        "qkv": nl * 2 * M * 3 * d * d,
+        "attention": nl * 4 * batch * ctx * ctx * d,
+        "out_proj": nl * 2 * M * d * d,
+        "fc1": nl * 2 * M * 4 * d * d,
+        "fc2": nl * 2 * M * 4 * d * d,
+    }
+
+
+def stage_launches(g):
+    nl = g["n_layer"]
+    return {"conv1": 1, "conv2": 1, "qkv": nl, "attention": nl, "out_proj": nl,
+            "fc1": nl, "fc2": nl, "layernorm": 2 * nl, "ln_post": 1, "prep": 1}
+
+
+def time_forward(enc, mel, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        enc.forward(mel)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = enc.forward(mel)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return dt, out
+
+
+def rowop_bandwidth(dev):
+    """Row kernels over rotating buffer sets > 256 MB, captured in a graph so
+    launch gaps do not count; returns GB/s per kernel (algorithmic bytes =
+    one read + one write of every element)."""
+    import torch
+    from wxhip import _lib as L
+    out = {}
+    specs = [
+        ("layernorm_1500x1280_bf16", (1500, 1280), 80),
+        ("gelu_erf_1500x5120_bf16", (1500, 5120), 24),
+        ("gelu_poly4_1500x5120_bf16", (1500, 5120), 24),
+        ("softmax_30000x1500_bf16", (30000, 1500), 4),
+    ]
+    for name, shape, nset in specs:
+        xs = [torch.randn(shape, device=dev.device).to(torch.bfloat16) for _ in range(nset)]
+        ys = [torch.empty_like(xs[0]) for _ in range(nset)]
+        g = torch.ones(shape[1], device=dev.device)
+        b = torch.zeros(shape[1], device=dev.device)
+
+        def run(i):
+            if name.startswith("layernorm"):
+                dev.layer_norm(xs[i], g, b, out=ys[i])
+            elif name.startswith("gelu_erf"):
+                dev.gelu(xs[i], L.WXH_GELU_ERF, out=ys[i])
+            elif name.startswith("gelu_poly4"):
+                dev.gelu(xs[i], L.WXH_GELU_POLY4_RNE, out=ys[i])
+            else:
+                dev.softmax_rows(xs[i], out=ys[i])
+
+        for i in range(nset):
+            run(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(nset):
+                run(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = 5
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per = e0.elapsed_time(e1) / 1e3 / (reps * nset)
+        nbytes = 2 * 2 * shape[0] * shape[1]
+        gbs = nbytes / per / 1e9
+        out[name] = {"us": round(per * 1e6, 2), "GB/s": round(gbs, 1),
+                     "hbm_frac": round(gbs * 1e9 / PEAK_HBM, 3),
+                     "working_set_MB": round(nset * nbytes / 1e6)}
+        del xs, ys, graph
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(W, n_mels):
+    """torch fp32 oracle on this host's cores: one warmup and two timed
+    forwards of one large-v3 sample (3000 mel frames)."""
+    import numpy as np
+    import torch
+    from oracle import encoder as OE
+    from wxhip import synth
+    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    mel = synth.make_mel(n_mels, 3000, seed=0)
+    OE.encoder_torch(W, mel)
+    ts = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        OE.encoder_torch(W, mel)
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    return {"value": round(3000 / t, 1), "unit": "mel-frames/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "1 of the 16 large-v3 mels (3000 frames, batch 1), torch fp32 "
+                      "encoder restatement, median of 2 after 1 warmup",
+            "ms_per_forward": round(t * 1e3, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="l16")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-rowops", action="store_true")
+    ap.add_argument("--no-latency", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the encoder shards as independent batch items; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import wxhip
+    from wxhip import synth
+
+    wl = WORKLOADS[args.workload]
+    B, T = wl["batch"], wl["n_frames"]
+    log(f"weights: large-v3 shape, seed 0 ...")
+    t0 = time.perf_counter()
+    W = synth.make_weights("large-v3")
+    log(f"  {time.perf_counter() - t0:.1f} s")
+    dev = wxhip.Device(0)
+    enc = wxhip.HipEncoder(dev, W)
+    log("weights uploaded")
+    mel = torch.from_numpy(synth.make_mel_batch(B, 128, T)).to(dev.device)
+
+    dt, out = time_forward(enc, mel, args.steps, args.warmup)
+    assert torch.isfinite(out).all().item()
+    frames = B * T
+    log(f"{args.workload}: {dt * 1e3:.2f} ms/forward, {frames / dt:.0f} mel-frames/s")
+
+    # per-stage device time of the same workload (HIP events, library stream)
+    profs = [enc.profile(mel) for _ in range(3)]
+    stages = {k: float(np.mean([p[k] for p in profs])) for k in profs[0]}
+    flops = stage_flops(LARGE, B, T)
+    launches = stage_launches(LARGE)
+    kern = {}
+    for k, ms in stages.items():
+        e = {"ms": round(ms, 3), "launches": launches[k]}
+        if k in flops and ms > 0:
+            tf = flops[k] / (ms / 1e3)
+            e.update(tflops=round(tf / 1e12, 1), mfma_frac=round(tf / PEAK_BF16, 4))
+        kern[k] = e
+    dom = max((k for k in flops), key=lambda k: stages[k])
+    per_launch_s = stages[dom] / 1e3 / launches[dom]
+    flop_per_launch = flops[dom] / launches[dom]
+    achieved = flop_per_launch / per_launch_s / 1e12
+    total_flops = sum(flops.values())
+
+    res = {
+        "metric": METRIC,
+        "value": round(frames / dt, 1),
+        "unit": "mel-frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded random-init large-v3-shaped weights N(0,0.02), "
+                "log-mels N(-0.3,0.5) clipped to [-1,1.5], seeds 0..15",
+        "config": {"workload": wl["name"], "batch": B, "n_frames": T,
+                   "ctx": (T - 1) // 2 + 1, "d_model": 1280, "n_head": 20, "n_layer": 32},
+        "encoder_tflops": round(total_flops / dt / 1e12, 1),
+        "encoder_mfma_frac": round(total_flops / dt / PEAK_BF16, 4),
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                     "flop_per_launch": flop_per_launch,
+                     "avg_launch_us": round(per_launch_s * 1e6, 2)},
+        "stages": kern,
+    }
+
+    if not args.no_latency and args.workload != "l1":
+        mel1 = mel[:1].contiguous() if T == 3000 else torch.from_numpy(
+            synth.make_mel(128, 3000, 0)[None]).to(dev.device)
+        dt1, _ = time_forward(enc, mel1, max(args.steps, 10), args.warmup)
+        res["latency_bs1_ms"] = round(dt1 * 1e3, 3)
+        f1 = sum(stage_flops(LARGE, 1, 3000).values())
+        res["latency_bs1_mfma_frac"] = round(f1 / dt1 / PEAK_BF16, 4)
+        log(f"l1 latency: {dt1 * 1e3:.2f} ms")
+    elif args.workload == "l1":
+        res["latency_bs1_ms"] = round(dt * 1e3, 3)
+
+    if not args.no_rowops:
+        res["rowops"] = rowop_bandwidth(dev)
+        log(f"rowops: {res['rowops']}")
+
+    del enc
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        log("cpu baseline (torch fp32, one large-v3 sample) ...")
+        res["cpu_baseline"] = cpu_baseline(W, 128)
+        log(f"  {res['cpu_baseline']}")
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

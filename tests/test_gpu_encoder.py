@@ -1,0 +1,174 @@
+"""The whole encoder on the GPU against the CPU torch fp32 oracle
+(oracle/encoder.py), and the drop-in surface around it.
+
+Gates (cosine over all output elements, synthetic seeded inputs):
+  tiny (4 layers, ctx 1500)          >= 0.9999
+  small (12 layers)                  >= 0.9999
+  large-v3 (32 layers, ctx 1500)     >= 0.994
+  reduced context (ctx 512)          >= 0.9999
+Size-independent properties: batch item b of a batched forward equals the
+same mel run alone, bit for bit; graph replay equals eager launch, bit for
+bit, replay after replay.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import case, cosine
+from oracle import encoder as OE
+from wxhip import _lib as L
+from wxhip import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    return synth.make_weights("tiny")
+
+
+def _enc(dev, W, **kw):
+    import wxhip
+    return wxhip.HipEncoder(dev, W, **kw)
+
+
+def _fwd(enc, mel, dev):
+    out = enc.forward(torch.from_numpy(np.ascontiguousarray(mel)).to(dev.device))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def test_tiny_encoder_cosine(dev, tiny):
+    case("encoder tiny 4 layers ctx 1500")
+    mel = synth.make_mel(80, 3000, seed=0)
+    got = _fwd(_enc(dev, tiny), mel, dev)
+    ref = OE.encoder_torch(tiny, mel)
+    c = cosine(got, ref)
+    print(f"tiny cosine {c:.8f} max|d| {np.abs(got - ref).max():.4g}")
+    assert got.shape == (1500, 384) and np.isfinite(got).all()
+    assert c >= 0.9999
+
+
+def test_tiny_encoder_poly4_mlp(dev, tiny):
+    """The reference's device MLP GELU (g4f poly4) in place of erf: held to
+    the reference's own accuracy floor (test_encoder_golden.py:43, 0.999)."""
+    case("encoder tiny poly4 MLP")
+    mel = synth.make_mel(80, 3000, seed=1)
+    got = _fwd(_enc(dev, tiny, mlp_gelu="poly4"), mel, dev)
+    assert cosine(got, OE.encoder_torch(tiny, mel)) >= 0.999
+
+
+def test_batch_items_independent_and_graph_replay(dev, tiny):
+    case("encoder tiny batch 3 vs single; graph vs eager")
+    mels = synth.make_mel_batch(3, 80, 3000)
+    enc = _enc(dev, tiny)
+    batched = _fwd(enc, mels, dev)
+    for b in range(3):
+        np.testing.assert_array_equal(batched[b], _fwd(enc, mels[b], dev))
+    # replays with eager work and syncs between them must all agree
+    first = _fwd(enc, mels, dev)
+    for _ in range(3):
+        torch.ones(1000, device=dev.device).sum().item()
+        np.testing.assert_array_equal(_fwd(enc, mels, dev), first)
+    enc.set_graph(False)
+    np.testing.assert_array_equal(_fwd(enc, mels, dev), first)
+
+
+def test_reduced_context_512(dev, tiny):
+    case("encoder tiny ctx 512")
+    mel = synth.make_mel(80, 1024, seed=2)
+    got = _fwd(_enc(dev, tiny), mel, dev)
+    assert got.shape == (512, 384)
+    assert cosine(got, OE.encoder_torch(tiny, mel)) >= 0.9999
+
+
+def test_small_encoder_cosine(dev):
+    case("encoder small 12 layers")
+    W = synth.make_weights("small")
+    mel = synth.make_mel(80, 3000, seed=0)
+    got = _fwd(_enc(dev, W), mel, dev)
+    c = cosine(got, OE.encoder_torch(W, mel))
+    print(f"small cosine {c:.8f}")
+    assert c >= 0.9999
+
+
+def test_large_v3_encoder_cosine(dev):
+    case("encoder large-v3 32 layers ctx 1500")
+    W = synth.make_weights("large-v3")
+    mel = synth.make_mel(128, 3000, seed=0)
+    got = _fwd(_enc(dev, W), mel, dev)
+    ref = OE.encoder_torch(W, mel)
+    c = cosine(got, ref)
+    print(f"large-v3 cosine {c:.8f}")
+    assert got.shape == (1500, 1280) and np.isfinite(got).all()
+    assert c >= 0.994
+
+
+def test_profile_stages(dev, tiny):
+    case("encoder profile")
+    enc = _enc(dev, tiny)
+    mel = torch.from_numpy(synth.make_mel(80, 3000, seed=0)).to(dev.device)
+    prof = enc.profile(mel)
+    assert set(prof) >= {"conv1", "qkv", "attention", "fc1", "fc2"}
+    assert all(v >= 0 for v in prof.values()) and prof["fc1"] > 0
+
+
+def test_dropin_encoder_graph_and_ops_paths(dev, tiny):
+    """encoder(W, mel, rt.matmul, rt.matmul, attn_fn=rt.attn_chain) as the
+    reference's callers drive it (run_raw_encoder.py:79-116)."""
+    import wxhip
+    from wxhip import encoder as E
+    case("drop-in encoder() graph + op paths")
+    W = synth.add_transposed(dict(tiny))
+    mel = synth.make_mel(80, 3000, seed=0)
+    ref = OE.encoder_torch(W, mel)
+    rt = wxhip.HipRT()
+    rt.register_weights([v for v in W.values() if isinstance(v, np.ndarray)])
+    kw = dict(n_layer=4, n_head=6, attn_fn=rt.attn_chain)
+    g = E.encoder(W, mel, rt.matmul, rt.matmul, prof={}, **kw)
+    assert cosine(g, ref) >= 0.9999 and not rt.fallbacks
+    # the same call with custom plugs runs op by op
+    o = E.encoder(W, mel, rt.matmul, rt.matmul, attn_fn=lambda *a: rt.attn_chain(*a),
+                  n_layer=4, n_head=6)
+    assert cosine(o, ref) >= 0.9999
+    assert cosine(o, g) >= 0.9999
+
+
+def test_fallback_on_chain_failure(dev, tiny):
+    """A failing attention chain degrades to the device-routed path, is
+    recorded, and the result still passes (test_encoder_golden.py:137-160)."""
+    import wxhip
+    from wxhip import encoder as E
+    case("fallback injection: attention chain")
+    W = dict(tiny)
+    mel = synth.make_mel(80, 3000, seed=0)
+    rt = wxhip.HipRT()
+
+    def boom(*a, **k):
+        raise RuntimeError("injected: chain unavailable")
+
+    rt._attn_chain_dev = boom
+    out = E.encoder(W, mel, rt.matmul, rt.matmul, n_layer=4, n_head=6,
+                    attn_fn=rt.attn_chain)
+    assert cosine(out, OE.encoder_torch(W, mel)) >= 0.9999
+    assert len(rt.fallbacks) == 1 and not rt.chain_ok
+
+
+def test_fallback_on_injected_c_abi_failure(dev, tiny):
+    """wxh_set_fail_inject(WXH_FAIL_ENCODER) makes the graph forward return
+    WXH_ERR_INJECTED before touching the device; encoder() records it and
+    finishes op by op."""
+    import wxhip
+    from wxhip import encoder as E
+    case("fallback injection: C ABI encoder")
+    mel = synth.make_mel(80, 3000, seed=0)
+    rt = wxhip.HipRT()
+    rt.dev.set_fail_inject(L.WXH_FAIL_ENCODER)
+    with pytest.raises(L.WxhError) as ei:
+        rt.encoder_forward(tiny, mel)
+    assert ei.value.code == L.WXH_ERR_INJECTED
+    out = E.encoder(tiny, mel, rt.matmul, rt.matmul, n_layer=4, n_head=6,
+                    attn_fn=rt.attn_chain)
+    assert not rt.graph_ok and len(rt.fallbacks) == 1
+    assert cosine(out, OE.encoder_torch(tiny, mel)) >= 0.9999
+    rt.dev.set_fail_inject(0)

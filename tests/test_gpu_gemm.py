@@ -1,0 +1,152 @@
+"""GPU parity of the MFMA GEMM (wxh_gemm_bf16) against an fp64 matmul of the
+same bf16-rounded operands (the textbook oracle for a bf16 x bf16 -> fp32
+GEMM; RawRT.matmul's contract, rawxrt.py:926-996).
+
+Tolerance: fp32 accumulation of K products can differ from the exact sum by
+at most ~K * 2^-24 * sum|a_k w_k|; the gate is 2e-4 * (|A| |W|^T), far below
+any indexing or layout error (those are O(1) relative).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import bits, case, cosine
+from oracle import bf16 as OB
+from oracle import rowops as OR
+from wxhip import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+
+def _operands(M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    A = OB.rb(rng.normal(0, 1, (M, K)).astype(np.float32))
+    W = OB.rb(rng.normal(0, 0.05, (N, K)).astype(np.float32))
+    b = rng.normal(0, 0.1, N).astype(np.float32)
+    return A, W, b
+
+
+def _exact(A, W, b=None):
+    r = A.astype(np.float64) @ W.astype(np.float64).T
+    if b is not None:
+        r += b
+    return r, np.abs(A).astype(np.float64) @ np.abs(W).astype(np.float64).T
+
+
+def _dev(x, dev, bf16=True):
+    t = torch.from_numpy(np.ascontiguousarray(x)).to(dev.device)
+    return t.to(torch.bfloat16) if bf16 else t
+
+
+SHAPES = [
+    (128, 128, 64),      # one tile
+    (1500, 1280, 1280),  # out-proj at batch 1 (M tail: 1500 = 11*128 + 92)
+    (1500, 3840, 1280),  # fused QKV
+    (300, 384, 240),     # conv1 of tiny: K = 3*80 is not a multiple of 64
+    (77, 200, 40),       # ragged everything
+    (1, 64, 8),          # smallest
+    (1500, 1280, 5120),  # fc2
+]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_f32_bias(dev, M, N, K):
+    case(f"gemm f32+bias M={M} N={N} K={K}")
+    A, W, b = _operands(M, N, K, seed=M + N + K)
+    C = dev.gemm(_dev(A, dev), _dev(W, dev), _dev(b, dev, False), L.WXH_EPI_F32)
+    got = C.cpu().numpy()
+    ref, mag = _exact(A, W, b)
+    err = np.abs(got - ref)
+    bad = err > 2e-4 * mag + 1e-6
+    if bad.any():
+        i, j = np.argwhere(bad)[0]
+        pytest.fail(f"{int(bad.sum())} elements off; first ({i},{j}) got {got[i, j]} "
+                    f"want {ref[i, j]}; max err {err.max()}")
+
+
+def test_gemm_structured_layout(dev):
+    """One-hot rows/columns pin the fragment layout: C[m, n] = A[m, k] W[n, k]
+    picks exactly one product, so a transposed or shifted fragment shows up
+    as a wrong index, not as noise."""
+    case("gemm one-hot layout probe")
+    M = N = 256
+    K = 256
+    A = np.zeros((M, K), np.float32)
+    W = np.zeros((N, K), np.float32)
+    for m in range(M):
+        A[m, m % K] = 1.0 + (m % 7)
+    for n in range(N):
+        W[n, (3 * n) % K] = 1.0 + (n % 5)
+    C = dev.gemm(_dev(A, dev), _dev(W, dev), None, L.WXH_EPI_F32).cpu().numpy()
+    np.testing.assert_array_equal(C, A @ W.T)
+
+
+def test_gemm_bf16_and_gelu_epilogues(dev):
+    M, N, K = 1500, 1536, 384
+    case(f"gemm bf16 epilogues M={M} N={N} K={K}")
+    A, W, b = _operands(M, N, K, seed=7)
+    ref, mag = _exact(A, W, b)
+    a, w, bb = _dev(A, dev), _dev(W, dev), _dev(b, dev, False)
+    # plain bf16: acc in fp32 then RNE -> within 1 ulp of the exact value
+    y = bits(dev.gemm(a, w, bb, L.WXH_EPI_BF16))
+    assert OB.ulp_diff(y, OB.round_rne(ref.astype(np.float32))).max() <= 1
+    # erf GELU epilogue against the exact GELU of the fp32 accumulator
+    acc = dev.gemm(a, w, bb, L.WXH_EPI_F32).cpu().numpy()
+    yg = bits(dev.gemm(a, w, bb, L.WXH_EPI_BF16_GELU_ERF))
+    assert OB.ulp_diff(yg, OB.round_rne(OR.gelu_erf(acc).astype(np.float32))).max() <= 1
+    # poly4 (g4f) epilogue: bit-exact given the same fp32 accumulator
+    yp = bits(dev.gemm(a, w, bb, L.WXH_EPI_BF16_GELU_POLY4))
+    np.testing.assert_array_equal(yp, OR.gelu_poly4(acc, "rne", f32_input=True))
+
+
+def test_gemm_residual_epilogue(dev):
+    M, N, K = 1500, 1280, 5120
+    case(f"gemm residual M={M} N={N} K={K}")
+    A, W, b = _operands(M, N, K, seed=11)
+    x0 = np.random.default_rng(12).normal(0, 1, (M, N)).astype(np.float32)
+    x = _dev(x0, dev, False)
+    dev.gemm(_dev(A, dev), _dev(W, dev), _dev(b, dev, False), L.WXH_EPI_RESID_F32, out=x)
+    ref, mag = _exact(A, W, b)
+    err = np.abs(x.cpu().numpy() - (x0 + ref))
+    assert (err <= 2e-4 * mag + 1e-5).all(), err.max()
+
+
+def test_gemm_strided_views(dev):
+    """Row strides != K / N (column bands of wider buffers)."""
+    case("gemm strided views")
+    A, W, b = _operands(200, 256, 128, seed=3)
+    Abig = torch.zeros(200, 512, dtype=torch.bfloat16, device=dev.device)
+    Abig[:, 64:192] = _dev(A, dev)
+    Cbig = torch.full((200, 1024), 5.0, dtype=torch.float32, device=dev.device)
+    dev.gemm(Abig[:, 64:192], _dev(W, dev), None, L.WXH_EPI_F32, out=Cbig[:, 256:512])
+    ref, mag = _exact(A, W)
+    got = Cbig.cpu().numpy()
+    assert (np.abs(got[:, 256:512] - ref) <= 2e-4 * mag + 1e-6).all()
+    assert (got[:, :256] == 5.0).all() and (got[:, 512:] == 5.0).all()
+
+
+def test_gemm_rejects_bad_shapes(dev):
+    a = torch.zeros(4, 12, dtype=torch.bfloat16, device=dev.device)
+    w = torch.zeros(4, 12, dtype=torch.bfloat16, device=dev.device)
+    with pytest.raises(L.WxhError) as ei:
+        dev.gemm(a, w)
+    assert ei.value.code == L.WXH_ERR_INVALID
+
+
+def test_hiprt_matmul_plugin(dev):
+    """RawRT.matmul's signature: fp32 host A (M,K) @ B (K,N) [+bias]."""
+    import wxhip
+    case("HipRT.matmul")
+    rt = wxhip.HipRT()
+    rng = np.random.default_rng(2)
+    A = rng.normal(0, 1, (300, 384)).astype(np.float32)
+    B = rng.normal(0, 0.05, (384, 640)).astype(np.float32)
+    bias = rng.normal(0, 0.1, 640).astype(np.float32)
+    rt.register_weights([B, bias])
+    out = rt.matmul(A, B, bias=bias)
+    ref = OB.rb(A).astype(np.float64) @ OB.rb(B).astype(np.float64) + bias
+    assert cosine(out, ref) > 0.999999
+    np.testing.assert_allclose(out, ref, rtol=1e-3, atol=1e-3)
+    assert rt.calls == 1
+    out2 = rt.matmul(A, B, bias=bias)
+    np.testing.assert_array_equal(out, out2)

@@ -1,0 +1,213 @@
+// Fused flash attention for gfx950: O = softmax(scale * Q K^T) V per head,
+// head dim 64, no causal mask, keys past T masked to -inf before the exp.
+//
+// Replaces the reference's attention chain RawRT.attn_chain /
+// _attn_chain_dev (src/rawxrt.py:813-891: QK^T GEMM -> windowed row softmax
+// -> PV GEMM through device buffers) and follows the online-softmax
+// recurrence of its fused variant (kernels/attn_fused.cc:7-20,
+// kernels/attn_mmul.cc:201-222): running max m, correction exp(m - m'),
+// running sum l, fp32 accumulator O, one divide at the end. No score matrix
+// ever reaches HBM.
+//
+// The reference scales q and k by hd^-1/4 each (npu_whisper_encoder.py:461);
+// here the product scale^2 = 1/sqrt(hd) is applied once to the fp32 scores,
+// which is the same function with one rounding less.
+//
+// Layout: Q, K [B*nh, Tp, 64] and Vt [B*nh, 64, Tp] bf16 (Tp = T rounded up
+// to 64, pad rows/columns finite). A workgroup owns 128 query rows of one
+// head (4 waves x 32 rows) and streams 64-key K/V tiles through LDS.
+// Scores are computed transposed, S^T = K Q^T with v_mfma_f32_32x32x16_bf16,
+// so a lane owns one query column and 16 keys per 32-key block: the row max
+// and row sum are lane-local plus one exchange between the two lane halves,
+// and the correction factor is one scalar per lane. P^T is repacked to bf16
+// in registers and multiplied as O^T += V^T P^T; V^T's k-slots are read from
+// LDS in exactly the key order the score fragment left in each lane.
+#include "common.h"
+#include "kernels.h"
+
+namespace wx {
+
+constexpr int kQB = 128;         // query rows per workgroup
+constexpr int kKB = kAttnKeyBlock;  // keys per LDS tile
+constexpr int kLD = 72;          // padded LDS row (elements)
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void attn_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ Vt, int n_head, int T, int Tp,
+    float scale_log2, void* __restrict__ O, int64_t ldo) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKB * kLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kHeadDim * kLD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int w = tid >> 6;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * n_head + h;
+  const int q0 = blockIdx.x * kQB + w * 32;
+  const uint16_t* Qh = Q + bh * Tp * kHeadDim;
+  const uint16_t* Kh = K + bh * Tp * kHeadDim;
+  const uint16_t* Vh = Vt + bh * kHeadDim * Tp;
+
+  int qrow = q0 + l32;
+  qrow = qrow < Tp ? qrow : Tp - 1;
+  bf16x8 qf[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    qf[kk] = *reinterpret_cast<const bf16x8*>(Qh + (int64_t)qrow * kHeadDim +
+                                              kk * 16 + half * 8);
+
+  f32x16 o[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int nkb = Tp / kKB;
+  for (int kb = 0; kb < nkb; ++kb) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + i * 256;
+      const int r = c >> 3, kc = (c & 7) * 8;
+      *reinterpret_cast<u32x4*>(&Ks[r * kLD + kc]) =
+          *reinterpret_cast<const u32x4*>(Kh + (int64_t)(kb * kKB + r) * kHeadDim + kc);
+      *reinterpret_cast<u32x4*>(&Vs[r * kLD + kc]) =
+          *reinterpret_cast<const u32x4*>(Vh + (int64_t)r * Tp + kb * kKB + kc);
+    }
+    __syncthreads();
+
+    // S^T for two 32-key blocks
+    f32x16 s[2];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[k2][r] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(
+            &Ks[(k2 * 32 + l32) * kLD + kk * 16 + half * 8]);
+        s[k2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[kk], s[k2], 0, 0, 0);
+      }
+    }
+    // scale (log2 domain), mask, block max
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb * kKB + k2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float val = key < T ? s[k2][r] * scale_log2 : -INFINITY;
+        s[k2][r] = val;
+        mx = fmaxf(mx, val);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = exp2f(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    uint32_t pk[2][8];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p0 = exp2f(s[k2][2 * j] - m_new);
+        const float p1 = exp2f(s[k2][2 * j + 1] - m_new);
+        l_run += p0 + p1;
+        pk[k2][j] = f2bf2(p0, p1);
+      }
+    m_run = m_new;
+
+    // O^T += V^T P^T over the 64 keys of the tile, 16 keys per MFMA
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int k2 = ks >> 1, sub = ks & 1;
+      const u32x4 pv = {pk[k2][4 * sub + 0], pk[k2][4 * sub + 1],
+                        pk[k2][4 * sub + 2], pk[k2][4 * sub + 3]};
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pv);
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const uint16_t* vrow = &Vs[(db * 32 + l32) * kLD + 16 * ks + 4 * half];
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+        const u32x4 vv = {lo[0], lo[1], hi[0], hi[1]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, vv), pb, o[db], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+
+  l_run += __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / l_run;
+  const int q = q0 + l32;
+  if (q >= T) return;
+  const int64_t orow = ((int64_t)b * T + q) * ldo + (int64_t)h * kHeadDim;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = db * 32 + 8 * g + 4 * half;
+      const float v0 = o[db][4 * g + 0] * inv, v1 = o[db][4 * g + 1] * inv;
+      const float v2 = o[db][4 * g + 2] * inv, v3 = o[db][4 * g + 3] * inv;
+      if (OUT_F32) {
+        const f32x4 vv = {v0, v1, v2, v3};
+        *reinterpret_cast<f32x4*>(static_cast<float*>(O) + orow + d0) = vv;
+      } else {
+        const u32x2 vv = {f2bf2(v0, v1), f2bf2(v2, v3)};
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(O) + orow + d0) = vv;
+      }
+    }
+}
+
+hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
+                            const uint16_t* Vt, int batch, int n_head, int T,
+                            float scale, void* O, int o_dtype, int64_t ldo,
+                            hipStream_t s) {
+  if (T <= 0 || batch <= 0 || n_head <= 0) return hipSuccess;
+  const int Tp = attn_padded_len(T);
+  dim3 grid((T + kQB - 1) / kQB, n_head, batch);
+  const float scale_log2 = scale * 1.4426950408889634f;
+  if (o_dtype == DT_F32)
+    attn_kernel<true><<<grid, 256, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
+  else
+    attn_kernel<false><<<grid, 256, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
+  return hipGetLastError();
+}
+
+// fp32 [B*T, nh*64] q/k/v rows -> Q, K [B*nh, Tp, 64] and Vt [B*nh, 64, Tp].
+__global__ __launch_bounds__(256) void pack_qkv_kernel(
+    const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, int64_t ld, int T, int n_head, int Tp,
+    uint16_t* __restrict__ Qo, uint16_t* __restrict__ Ko,
+    uint16_t* __restrict__ Vo) {
+  const int t = blockIdx.x;
+  const int b = blockIdx.y;
+  const int d = n_head * kHeadDim;
+  const int64_t src = ((int64_t)b * T + t) * ld;
+  for (int n = threadIdx.x; n < d; n += 256) {
+    const int h = n >> 6, dd = n & 63;
+    const int64_t bh = (int64_t)b * n_head + h;
+    Qo[(bh * Tp + t) * kHeadDim + dd] = f2bf(q[src + n]);
+    Ko[(bh * Tp + t) * kHeadDim + dd] = f2bf(k[src + n]);
+    Vo[(bh * kHeadDim + dd) * Tp + t] = f2bf(v[src + n]);
+  }
+}
+
+hipError_t launch_pack_qkv(const float* q, const float* k, const float* v,
+                           int64_t ld, int batch, int T, int n_head,
+                           uint16_t* Q, uint16_t* K, uint16_t* Vt,
+                           hipStream_t s) {
+  if (T <= 0 || batch <= 0) return hipSuccess;
+  dim3 grid(T, batch);
+  pack_qkv_kernel<<<grid, 256, 0, s>>>(q, k, v, ld, T, n_head,
+                                       attn_padded_len(T), Q, K, Vt);
+  return hipGetLastError();
+}
+
+}  // namespace wx

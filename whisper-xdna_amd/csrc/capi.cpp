@@ -1,0 +1,849 @@
+// C ABI of libwxhip.so: argument checking, error reporting, the context and
+// the encoder orchestrator (device-resident weights, workspace, hipGraph).
+//
+// The orchestrator replaces the reference's Python-driven per-call device
+// round trips (src/rawxrt.py: mm_start/mm_finish, _attn_chain_dev, _mlp_dev)
+// with one stream of kernels over device-resident tensors:
+//   prep_mel -> conv1 (GEMM, GELU) -> conv2 (GEMM, GELU, + pos-emb) ->
+//   per layer [LN -> QKV GEMM (head split) -> attention -> out GEMM (+x) ->
+//              LN -> fc1 GEMM (GELU) -> fc2 GEMM (+x)] -> ln_post
+// The residual stream x stays fp32 in HBM (as the reference keeps it fp32 on
+// the host, npu_whisper_encoder.py:512-527); GEMM inputs are bf16.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/wxhip.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define WXH_HIP(call)                                                      \
+  do {                                                                     \
+    hipError_t e_ = (call);                                                \
+    if (e_ != hipSuccess)                                                  \
+      return fail(WXH_ERR_HIP, "%s: %s (%s:%d)", #call, hipGetErrorString(e_), \
+                  __FILE__, __LINE__);                                     \
+  } while (0)
+
+#define WXH_REQUIRE(cond, ...)                          \
+  do {                                                  \
+    if (!(cond)) return fail(WXH_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+struct wxh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint32_t fail_mask = 0;
+};
+
+namespace {
+
+hipStream_t pick(wxh_ctx* c, void* s) {
+  return s ? static_cast<hipStream_t>(s) : c->stream;
+}
+
+int check_ctx(wxh_ctx* c, uint32_t bit, const char* what) {
+  if (!c) return fail(WXH_ERR_INVALID, "%s: null context", what);
+  if (c->fail_mask & bit)
+    return fail(WXH_ERR_INJECTED, "%s: injected failure (mask 0x%x)", what,
+                c->fail_mask);
+  hipError_t e = hipSetDevice(c->device);
+  if (e != hipSuccess)
+    return fail(WXH_ERR_HIP, "%s: hipSetDevice: %s", what, hipGetErrorString(e));
+  return WXH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wxh_version(void) { return "wxhip 0.1 gfx950"; }
+
+const char* wxh_last_error(void) { return g_err.c_str(); }
+
+int wxh_create(int device, wxh_ctx** out) {
+  WXH_REQUIRE(out, "wxh_create: out is null");
+  int n = 0;
+  WXH_HIP(hipGetDeviceCount(&n));
+  WXH_REQUIRE(device >= 0 && device < n, "wxh_create: device %d of %d", device, n);
+  WXH_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  WXH_HIP(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(WXH_ERR_UNSUPPORTED, "wxh_create: device %d is %s, built for gfx950",
+                device, prop.gcnArchName);
+  auto* c = new wxh_ctx;
+  c->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return fail(WXH_ERR_HIP, "wxh_create: hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  *out = c;
+  return WXH_OK;
+}
+
+int wxh_destroy(wxh_ctx* c) {
+  if (!c) return WXH_OK;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+  return WXH_OK;
+}
+
+int wxh_set_fail_inject(wxh_ctx* c, uint32_t mask) {
+  WXH_REQUIRE(c, "wxh_set_fail_inject: null context");
+  c->fail_mask = mask;
+  return WXH_OK;
+}
+
+int wxh_get_stream(wxh_ctx* c, void** stream) {
+  WXH_REQUIRE(c && stream, "wxh_get_stream: null argument");
+  *stream = c->stream;
+  return WXH_OK;
+}
+
+int wxh_synchronize(wxh_ctx* c) {
+  WXH_REQUIRE(c, "wxh_synchronize: null context");
+  WXH_HIP(hipSetDevice(c->device));
+  WXH_HIP(hipStreamSynchronize(c->stream));
+  return WXH_OK;
+}
+
+// ------------------------------------------------------------------ row ops
+
+int wxh_layernorm(wxh_ctx* c, const void* x, int x_dtype, int64_t ldx,
+                  const float* resid, int64_t ldr, float* sum_out,
+                  int64_t ld_sum, const float* gamma, const float* beta,
+                  float eps, void* y, int y_dtype, int64_t ldy, int rows,
+                  int cols, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_ROWOP, "wxh_layernorm")) return r;
+  WXH_REQUIRE(x && y, "wxh_layernorm: null x or y");
+  WXH_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= wx::kMaxRowCols,
+              "wxh_layernorm: cols=%d must be a positive multiple of 8 <= %d", cols,
+              wx::kMaxRowCols);
+  WXH_REQUIRE(x_dtype == WXH_BF16 || x_dtype == WXH_F32, "wxh_layernorm: x_dtype");
+  WXH_REQUIRE(y_dtype == WXH_BF16 || y_dtype == WXH_F32, "wxh_layernorm: y_dtype");
+  WXH_REQUIRE(ldx >= cols && ldy >= cols && ldx % 8 == 0 && ldy % 8 == 0,
+              "wxh_layernorm: row strides must be >= cols and multiples of 8");
+  WXH_REQUIRE(aligned16(x) && aligned16(y), "wxh_layernorm: x/y must be 16-byte aligned");
+  WXH_REQUIRE(!resid || (ldr >= cols && ldr % 8 == 0 && aligned16(resid)),
+              "wxh_layernorm: resid stride/alignment");
+  WXH_REQUIRE(!sum_out || (resid && ld_sum >= cols && ld_sum % 8 == 0 && aligned16(sum_out)),
+              "wxh_layernorm: sum_out needs resid and an aligned stride");
+  WXH_REQUIRE(!gamma || aligned16(gamma), "wxh_layernorm: gamma alignment");
+  WXH_REQUIRE(!beta || aligned16(beta), "wxh_layernorm: beta alignment");
+  WXH_HIP(wx::launch_layernorm(x, x_dtype, ldx, resid, ldr, sum_out, ld_sum, gamma,
+                               beta, eps, y, y_dtype, ldy, rows, cols, pick(c, stream)));
+  return WXH_OK;
+}
+
+int wxh_gelu(wxh_ctx* c, const void* x, int x_dtype, int64_t ldx, uint16_t* y,
+             int64_t ldy, int rows, int cols, int variant, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_ROWOP, "wxh_gelu")) return r;
+  WXH_REQUIRE(x && y, "wxh_gelu: null x or y");
+  WXH_REQUIRE(rows >= 0 && cols >= 0 && ldx >= cols && ldy >= cols,
+              "wxh_gelu: bad shape rows=%d cols=%d ldx=%lld ldy=%lld", rows, cols,
+              (long long)ldx, (long long)ldy);
+  WXH_REQUIRE(x_dtype == WXH_BF16 || x_dtype == WXH_F32, "wxh_gelu: x_dtype");
+  WXH_REQUIRE(variant >= WXH_GELU_ERF && variant <= WXH_GELU_POLY4_TRUNC,
+              "wxh_gelu: unknown variant %d", variant);
+  WXH_REQUIRE(!(variant == WXH_GELU_POLY4_TRUNC && x_dtype == WXH_F32),
+              "wxh_gelu: the truncating poly4 (g4) takes bf16 input");
+  WXH_HIP(wx::launch_gelu(x, x_dtype, ldx, y, ldy, rows, cols, variant, pick(c, stream)));
+  return WXH_OK;
+}
+
+int wxh_softmax_rows(wxh_ctx* c, const uint16_t* x, int64_t ldx, uint16_t* y,
+                     int64_t ldy, int rows, int valid, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_ROWOP, "wxh_softmax_rows")) return r;
+  WXH_REQUIRE(x && y, "wxh_softmax_rows: null x or y");
+  WXH_REQUIRE(rows >= 0 && valid > 0 && ldx >= valid && ldy >= valid,
+              "wxh_softmax_rows: bad shape rows=%d valid=%d", rows, valid);
+  WXH_HIP(wx::launch_softmax(x, ldx, y, ldy, rows, valid, pick(c, stream)));
+  return WXH_OK;
+}
+
+int wxh_convert_f32_bf16(wxh_ctx* c, const float* x, int64_t ldx, uint16_t* y,
+                         int64_t ldy, int rows, int cols, int transpose,
+                         void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_ROWOP, "wxh_convert_f32_bf16")) return r;
+  WXH_REQUIRE(x && y && rows >= 0 && cols >= 0 && ldx >= cols &&
+                  ldy >= (transpose ? rows : cols),
+              "wxh_convert_f32_bf16: bad arguments");
+  WXH_HIP(wx::launch_convert(x, ldx, y, ldy, rows, cols, transpose != 0, pick(c, stream)));
+  return WXH_OK;
+}
+
+// ------------------------------------------------------------------ GEMM
+
+int wxh_gemm_bf16(wxh_ctx* c, int M, int N, int K, const uint16_t* A,
+                  int64_t lda, const uint16_t* W, int64_t ldw,
+                  const float* bias, void* C, int64_t ldc, int epilogue,
+                  void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_GEMM, "wxh_gemm_bf16")) return r;
+  WXH_REQUIRE(A && W && C, "wxh_gemm_bf16: null operand");
+  WXH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "wxh_gemm_bf16: negative size");
+  WXH_REQUIRE(K % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && lda >= K && ldw >= K,
+              "wxh_gemm_bf16: K=%d lda=%lld ldw=%lld must be multiples of 8 (>= K)", K,
+              (long long)lda, (long long)ldw);
+  WXH_REQUIRE(ldc >= N, "wxh_gemm_bf16: ldc < N");
+  WXH_REQUIRE(aligned16(A) && aligned16(W), "wxh_gemm_bf16: A/W must be 16-byte aligned");
+  wx::EpiParams e;
+  e.out = C;
+  e.ldo = ldc;
+  e.bias = bias;
+  int mode;
+  switch (epilogue) {
+    case WXH_EPI_F32: mode = wx::EPI_F32; break;
+    case WXH_EPI_BF16: mode = wx::EPI_BF16; break;
+    case WXH_EPI_BF16_GELU_ERF: mode = wx::EPI_BF16; e.gelu = wx::GELU_ERF; break;
+    case WXH_EPI_BF16_GELU_POLY4: mode = wx::EPI_BF16; e.gelu = wx::GELU_POLY4_RNE; break;
+    case WXH_EPI_RESID_F32: mode = wx::EPI_RESID; break;
+    default: return fail(WXH_ERR_INVALID, "wxh_gemm_bf16: unknown epilogue %d", epilogue);
+  }
+  wx::GemmA a{A, lda, M > 0 ? M : 1, 0};
+  WXH_HIP(wx::launch_gemm(M, N, K, a, W, ldw, mode, e, pick(c, stream)));
+  return WXH_OK;
+}
+
+// ------------------------------------------------------------------ attention
+
+int wxh_attention_padded_len(int T) { return wx::attn_padded_len(T); }
+
+int wxh_pack_qkv(wxh_ctx* c, const float* q, const float* k, const float* v,
+                 int64_t ld, int batch, int T, int n_head, uint16_t* Q,
+                 uint16_t* K, uint16_t* Vt, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_ATTN, "wxh_pack_qkv")) return r;
+  WXH_REQUIRE(q && k && v && Q && K && Vt, "wxh_pack_qkv: null pointer");
+  WXH_REQUIRE(batch >= 0 && T >= 0 && n_head > 0 && ld >= (int64_t)n_head * 64,
+              "wxh_pack_qkv: bad shape");
+  WXH_HIP(wx::launch_pack_qkv(q, k, v, ld, batch, T, n_head, Q, K, Vt, pick(c, stream)));
+  return WXH_OK;
+}
+
+int wxh_attention(wxh_ctx* c, const uint16_t* Q, const uint16_t* K,
+                  const uint16_t* Vt, int batch, int n_head, int T, float scale,
+                  void* O, int o_dtype, int64_t ldo, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_ATTN, "wxh_attention")) return r;
+  WXH_REQUIRE(Q && K && Vt && O, "wxh_attention: null pointer");
+  WXH_REQUIRE(batch >= 0 && n_head > 0 && T >= 0, "wxh_attention: bad shape");
+  WXH_REQUIRE(o_dtype == WXH_BF16 || o_dtype == WXH_F32, "wxh_attention: o_dtype");
+  WXH_REQUIRE(ldo >= (int64_t)n_head * 64 && ldo % 4 == 0,
+              "wxh_attention: ldo must be >= n_head*64 and a multiple of 4");
+  WXH_REQUIRE(aligned16(Q) && aligned16(K) && aligned16(Vt) && aligned16(O),
+              "wxh_attention: operands must be 16-byte aligned");
+  WXH_HIP(wx::launch_attention(Q, K, Vt, batch, n_head, T, scale, O, o_dtype, ldo,
+                               pick(c, stream)));
+  return WXH_OK;
+}
+
+}  // extern "C"
+
+// ====================================================================== encoder
+
+namespace {
+
+struct LayerW {
+  uint16_t* wqkv = nullptr;  // [3d, d]
+  uint16_t* wo = nullptr;    // [d, d]
+  uint16_t* w1 = nullptr;    // [ffn, d]
+  uint16_t* w2 = nullptr;    // [d, ffn]
+  float* bqkv = nullptr;     // [3d] (key part zero)
+  float* bo = nullptr;
+  float* b1 = nullptr;
+  float* b2 = nullptr;
+  float* ln1_g = nullptr;
+  float* ln1_b = nullptr;
+  float* ln2_g = nullptr;
+  float* ln2_b = nullptr;
+};
+
+enum Stage {
+  ST_PREP = 0, ST_CONV1, ST_CONV2, ST_LN, ST_QKV, ST_ATTN, ST_OUT, ST_FC1,
+  ST_FC2, ST_LNPOST, ST_COUNT
+};
+
+}  // namespace
+
+struct wxh_encoder {
+  wxh_ctx* ctx = nullptr;
+  wxh_encoder_dims dims{};
+  int ffn = 0;
+  uint16_t* conv1_w = nullptr;  // [d, 3*n_mels], K index j*n_mels + c
+  uint16_t* conv2_w = nullptr;  // [d, 3*d], K index j*d + c
+  float* conv1_b = nullptr;
+  float* conv2_b = nullptr;
+  float* pos = nullptr;  // [n_ctx, d]
+  float* lnp_g = nullptr;
+  float* lnp_b = nullptr;
+  std::vector<LayerW> layers;
+  std::map<std::string, bool> have;
+  std::vector<void*> allocs;
+  // staging for fp32 uploads
+  float* stage = nullptr;
+  size_t stage_elems = 0;
+  // workspace; capacity in elements of the largest shape seen so far
+  int64_t cap_mel = 0, cap_x1 = 0, cap_x = 0, cap_qkv = 0, cap_f = 0;
+  uint16_t* melT = nullptr;  // [B, T+2, n_mels]
+  uint16_t* x1 = nullptr;    // [B, T+2, d]
+  float* x = nullptr;        // [B*ctx, d]
+  uint16_t* h = nullptr;     // [B*ctx, d]
+  uint16_t* q = nullptr;     // [B*nh, Tp, 64]
+  uint16_t* k = nullptr;
+  uint16_t* vt = nullptr;    // [B*nh, 64, Tp]
+  uint16_t* o = nullptr;     // [B*ctx, d]
+  uint16_t* f = nullptr;     // [B*ctx, ffn]
+  std::vector<void*> ws_allocs;
+  bool use_graph = true;
+  std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+};
+
+namespace {
+
+template <class T>
+int dalloc(std::vector<void*>& list, T** p, size_t count, bool zero) {
+  void* d = nullptr;
+  hipError_t e = hipMalloc(&d, count * sizeof(T) + 256);
+  if (e != hipSuccess)
+    return fail(WXH_ERR_HIP, "hipMalloc(%zu bytes): %s", count * sizeof(T),
+                hipGetErrorString(e));
+  if (zero) {
+    e = hipMemset(d, 0, count * sizeof(T) + 256);
+    if (e != hipSuccess) {
+      (void)hipFree(d);
+      return fail(WXH_ERR_HIP, "hipMemset: %s", hipGetErrorString(e));
+    }
+  }
+  list.push_back(d);
+  *p = static_cast<T*>(d);
+  return WXH_OK;
+}
+
+void free_list(std::vector<void*>& list) {
+  for (void* p : list) (void)hipFree(p);
+  list.clear();
+}
+
+void drop_graphs(wxh_encoder* E) {
+  for (auto& kv : E->graphs) (void)hipGraphExecDestroy(kv.second);
+  E->graphs.clear();
+}
+
+int ensure_stage(wxh_encoder* E, size_t n) {
+  if (E->stage_elems >= n) return WXH_OK;
+  if (E->stage) (void)hipFree(E->stage);
+  E->stage = nullptr;
+  E->stage_elems = 0;
+  WXH_HIP(hipMalloc(&E->stage, n * sizeof(float)));
+  E->stage_elems = n;
+  return WXH_OK;
+}
+
+// host fp32 [rows, cols] -> device bf16 via the conversion kernel (RNE)
+int upload_bf16(wxh_encoder* E, uint16_t* dst, const float* host, int rows, int cols) {
+  const size_t n = (size_t)rows * cols;
+  if (int r = ensure_stage(E, n)) return r;
+  hipStream_t s = E->ctx->stream;
+  WXH_HIP(hipMemcpyAsync(E->stage, host, n * sizeof(float), hipMemcpyHostToDevice, s));
+  WXH_HIP(wx::launch_convert(E->stage, cols, dst, cols, rows, cols, false, s));
+  WXH_HIP(hipStreamSynchronize(s));
+  return WXH_OK;
+}
+
+int upload_f32(wxh_encoder* E, float* dst, const float* host, size_t n) {
+  WXH_HIP(hipMemcpy(dst, host, n * sizeof(float), hipMemcpyHostToDevice));
+  return WXH_OK;
+}
+
+bool shape_is(const int64_t* shape, int ndim, std::initializer_list<int64_t> want) {
+  if ((size_t)ndim != want.size()) return false;
+  int i = 0;
+  for (int64_t w : want)
+    if (shape[i++] != w) return false;
+  return true;
+}
+
+std::vector<std::string> required_names(const wxh_encoder_dims& d) {
+  std::vector<std::string> v = {"conv1.weight", "conv1.bias", "conv2.weight",
+                                "conv2.bias", "positional_embedding",
+                                "ln_post.weight", "ln_post.bias"};
+  for (int L = 0; L < d.n_layer; ++L) {
+    const std::string p = "blocks." + std::to_string(L) + ".";
+    for (const char* s :
+         {"attn_ln.weight", "attn_ln.bias", "attn.query.weight", "attn.query.bias",
+          "attn.key.weight", "attn.value.weight", "attn.value.bias", "attn.out.weight",
+          "attn.out.bias", "mlp_ln.weight", "mlp_ln.bias", "mlp.0.weight", "mlp.0.bias",
+          "mlp.2.weight", "mlp.2.bias"})
+      v.push_back(p + s);
+  }
+  return v;
+}
+
+int ensure_workspace(wxh_encoder* E, int batch, int frames) {
+  const auto& D = E->dims;
+  const int64_t B = batch, T = frames;
+  const int64_t ctx = (T - 1) / 2 + 1;
+  const int64_t tp = wx::attn_padded_len((int)ctx);
+  const int64_t need_mel = B * (T + 2) * D.n_mels;
+  const int64_t need_x1 = B * (T + 2) * D.d_model;
+  const int64_t need_x = B * ctx * D.d_model;
+  const int64_t need_qkv = B * D.n_head * tp * 64;
+  const int64_t need_f = B * ctx * E->ffn;
+  if (need_mel <= E->cap_mel && need_x1 <= E->cap_x1 && need_x <= E->cap_x &&
+      need_qkv <= E->cap_qkv && need_f <= E->cap_f)
+    return WXH_OK;
+  drop_graphs(E);
+  free_list(E->ws_allocs);
+  E->cap_mel = E->cap_x1 = E->cap_x = E->cap_qkv = E->cap_f = 0;
+  auto& L = E->ws_allocs;
+  // pads (conv rows, attention key/query tails) must hold finite values:
+  // everything starts zeroed, and later writes only ever store finite bf16
+  if (int r = dalloc(L, &E->melT, need_mel, true)) return r;
+  if (int r = dalloc(L, &E->x1, need_x1, true)) return r;
+  if (int r = dalloc(L, &E->x, need_x, true)) return r;
+  if (int r = dalloc(L, &E->h, need_x, true)) return r;
+  if (int r = dalloc(L, &E->q, need_qkv, true)) return r;
+  if (int r = dalloc(L, &E->k, need_qkv, true)) return r;
+  if (int r = dalloc(L, &E->vt, need_qkv, true)) return r;
+  if (int r = dalloc(L, &E->o, need_x, true)) return r;
+  if (int r = dalloc(L, &E->f, need_f, true)) return r;
+  E->cap_mel = need_mel;
+  E->cap_x1 = need_x1;
+  E->cap_x = need_x;
+  E->cap_qkv = need_qkv;
+  E->cap_f = need_f;
+  return WXH_OK;
+}
+
+// Zero rows 0 and T+1 of every batch item of the padded conv1 output (the
+// conv2 im2col reads them as the zero padding).
+__global__ void zero_pad_rows_kernel(uint16_t* x1, int T, int d) {
+  const int b = blockIdx.x;
+  uint16_t* base = x1 + (int64_t)b * (T + 2) * d;
+  for (int c = threadIdx.x; c < d; c += blockDim.x) {
+    base[c] = 0;
+    base[(int64_t)(T + 1) * d + c] = 0;
+  }
+}
+
+struct StageTimer {
+  std::vector<std::pair<int, hipEvent_t>> marks;
+  hipEvent_t start = nullptr;
+};
+
+// Launch the forward body (conv1 .. last layer). Stage events are recorded
+// after each launch when `timer` is set (un-graphed profiling only).
+int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* timer) {
+  const auto& D = E->dims;
+  const int d = D.d_model, nh = D.n_head, T = frames;
+  const int ctx = (T - 1) / 2 + 1;
+  const int tp = wx::attn_padded_len(ctx);
+  const int M = batch * ctx;
+  auto mark = [&](int stage) -> int {
+    if (!timer) return WXH_OK;
+    hipEvent_t ev;
+    WXH_HIP(hipEventCreate(&ev));
+    WXH_HIP(hipEventRecord(ev, s));
+    timer->marks.push_back({stage, ev});
+    return WXH_OK;
+  };
+
+  {  // conv1: window of 3 padded mel rows, GELU, into padded x1 rows
+    wx::GemmA a{E->melT, D.n_mels, T, (int64_t)(T + 2) * D.n_mels};
+    wx::EpiParams e;
+    e.out = E->x1;
+    e.ldo = d;
+    e.bias = E->conv1_b;
+    e.rows_per_batch = T;
+    e.out_batch_stride = (int64_t)(T + 2) * d;
+    WXH_HIP(wx::launch_gemm(batch * T, d, 3 * D.n_mels, a, E->conv1_w, 3 * D.n_mels,
+                            wx::EPI_CONV1, e, s));
+    if (int r = mark(ST_CONV1)) return r;
+  }
+  {  // conv2: stride-2 window of 3 padded x1 rows, GELU, + positional embedding
+    wx::GemmA a{E->x1, 2 * (int64_t)d, ctx, (int64_t)(T + 2) * d};
+    wx::EpiParams e;
+    e.out = E->x;
+    e.ldo = d;
+    e.bias = E->conv2_b;
+    e.aux = E->pos;
+    e.rows_per_batch = ctx;
+    WXH_HIP(wx::launch_gemm(M, d, 3 * d, a, E->conv2_w, 3 * d, wx::EPI_CONV2, e, s));
+    if (int r = mark(ST_CONV2)) return r;
+  }
+  const float scale = 1.0f / 8.0f;  // (hd^-1/4)^2 with hd = 64
+  for (int l = 0; l < D.n_layer; ++l) {
+    const LayerW& W = E->layers[l];
+    WXH_HIP(wx::launch_layernorm(E->x, wx::DT_F32, d, nullptr, 0, nullptr, 0, W.ln1_g,
+                                 W.ln1_b, 1e-5f, E->h, wx::DT_BF16, d, M, d, s));
+    if (int r = mark(ST_LN)) return r;
+    {
+      wx::GemmA a{E->h, d, M, 0};
+      wx::EpiParams e;
+      e.bias = W.bqkv;
+      e.q = E->q;
+      e.k = E->k;
+      e.vt = E->vt;
+      e.n_head = nh;
+      e.t_pad = tp;
+      e.d_model = d;
+      e.rows_per_batch = ctx;
+      WXH_HIP(wx::launch_gemm(M, 3 * d, d, a, W.wqkv, d, wx::EPI_QKV, e, s));
+      if (int r = mark(ST_QKV)) return r;
+    }
+    WXH_HIP(wx::launch_attention(E->q, E->k, E->vt, batch, nh, ctx, scale, E->o,
+                                 wx::DT_BF16, d, s));
+    if (int r = mark(ST_ATTN)) return r;
+    {
+      wx::GemmA a{E->o, d, M, 0};
+      wx::EpiParams e;
+      e.out = E->x;
+      e.ldo = d;
+      e.bias = W.bo;
+      WXH_HIP(wx::launch_gemm(M, d, d, a, W.wo, d, wx::EPI_RESID, e, s));
+      if (int r = mark(ST_OUT)) return r;
+    }
+    WXH_HIP(wx::launch_layernorm(E->x, wx::DT_F32, d, nullptr, 0, nullptr, 0, W.ln2_g,
+                                 W.ln2_b, 1e-5f, E->h, wx::DT_BF16, d, M, d, s));
+    if (int r = mark(ST_LN)) return r;
+    {
+      wx::GemmA a{E->h, d, M, 0};
+      wx::EpiParams e;
+      e.out = E->f;
+      e.ldo = E->ffn;
+      e.bias = W.b1;
+      e.gelu = D.mlp_gelu == WXH_GELU_POLY4_RNE ? wx::GELU_POLY4_RNE : wx::GELU_ERF;
+      WXH_HIP(wx::launch_gemm(M, E->ffn, d, a, W.w1, d, wx::EPI_BF16, e, s));
+      if (int r = mark(ST_FC1)) return r;
+    }
+    {
+      wx::GemmA a{E->f, E->ffn, M, 0};
+      wx::EpiParams e;
+      e.out = E->x;
+      e.ldo = d;
+      e.bias = W.b2;
+      WXH_HIP(wx::launch_gemm(M, d, E->ffn, a, W.w2, E->ffn, wx::EPI_RESID, e, s));
+      if (int r = mark(ST_FC2)) return r;
+    }
+  }
+  return WXH_OK;
+}
+
+int check_forward_args(wxh_encoder* E, int batch, int frames) {
+  if (!E) return fail(WXH_ERR_INVALID, "encoder: null handle");
+  if (int r = check_ctx(E->ctx, WXH_FAIL_ENCODER, "wxh_encoder_forward")) return r;
+  if (wxh_encoder_ready(E) != WXH_OK) return WXH_ERR_STATE;
+  WXH_REQUIRE(batch > 0 && frames >= 3, "encoder: batch=%d n_frames=%d", batch, frames);
+  const int ctx = (frames - 1) / 2 + 1;
+  WXH_REQUIRE(ctx <= E->dims.n_ctx,
+              "encoder: n_frames=%d gives ctx=%d > positional embedding %d", frames,
+              ctx, E->dims.n_ctx);
+  return WXH_OK;
+}
+
+int forward_impl(wxh_encoder* E, const float* mel, int batch, int frames, float* out,
+                 hipStream_t s, StageTimer* timer) {
+  const auto& D = E->dims;
+  const int ctx = (frames - 1) / 2 + 1;
+  if (int r = ensure_workspace(E, batch, frames)) return r;
+  WXH_HIP(wx::launch_prep_mel(mel, batch, D.n_mels, frames, E->melT, s));
+  zero_pad_rows_kernel<<<batch, 256, 0, s>>>(E->x1, frames, D.d_model);
+  WXH_HIP(hipGetLastError());
+  if (timer) {
+    hipEvent_t ev;
+    WXH_HIP(hipEventCreate(&ev));
+    WXH_HIP(hipEventRecord(ev, s));
+    timer->marks.push_back({ST_PREP, ev});
+  }
+  if (E->use_graph && !timer) {
+    auto key = std::make_pair(batch, frames);
+    auto it = E->graphs.find(key);
+    if (it == E->graphs.end()) {
+      // capture on the context's stream (recording only, nothing runs);
+      // the instantiated graph is then launched on `s`
+      hipStream_t cs = E->ctx->stream;
+      WXH_HIP(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
+      int r = run_body(E, batch, frames, cs, nullptr);
+      hipGraph_t g = nullptr;
+      hipError_t ee = hipStreamEndCapture(cs, &g);
+      if (r != WXH_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return r;
+      }
+      if (ee != hipSuccess)
+        return fail(WXH_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ee));
+      hipGraphExec_t ex = nullptr;
+      ee = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (ee != hipSuccess)
+        return fail(WXH_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ee));
+      it = E->graphs.emplace(key, ex).first;
+    }
+    WXH_HIP(hipGraphLaunch(it->second, s));
+  } else {
+    if (int r = run_body(E, batch, frames, s, timer)) return r;
+  }
+  WXH_HIP(wx::launch_layernorm(E->x, wx::DT_F32, D.d_model, nullptr, 0, nullptr, 0,
+                               E->lnp_g, E->lnp_b, 1e-5f, out, wx::DT_F32, D.d_model,
+                               batch * ctx, D.d_model, s));
+  if (timer) {
+    hipEvent_t ev;
+    WXH_HIP(hipEventCreate(&ev));
+    WXH_HIP(hipEventRecord(ev, s));
+    timer->marks.push_back({ST_LNPOST, ev});
+  }
+  return WXH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wxh_encoder_create(wxh_ctx* c, const wxh_encoder_dims* dims, wxh_encoder** out) {
+  if (int r = check_ctx(c, 0, "wxh_encoder_create")) return r;
+  WXH_REQUIRE(dims && out, "wxh_encoder_create: null argument");
+  const auto& D = *dims;
+  WXH_REQUIRE(D.n_head > 0 && D.d_model == D.n_head * 64,
+              "wxh_encoder_create: d_model=%d must be n_head*64 (n_head=%d)", D.d_model,
+              D.n_head);
+  WXH_REQUIRE(D.n_mels > 0 && D.n_mels % 8 == 0, "wxh_encoder_create: n_mels=%d", D.n_mels);
+  WXH_REQUIRE(D.n_layer >= 0 && D.n_ctx > 0, "wxh_encoder_create: n_layer/n_ctx");
+  WXH_REQUIRE(D.d_model <= wx::kMaxRowCols, "wxh_encoder_create: d_model too large");
+  WXH_REQUIRE(D.mlp_gelu == WXH_GELU_ERF || D.mlp_gelu == WXH_GELU_POLY4_RNE,
+              "wxh_encoder_create: mlp_gelu must be ERF or POLY4_RNE");
+  auto* E = new wxh_encoder;
+  E->ctx = c;
+  E->dims = D;
+  E->ffn = 4 * D.d_model;
+  const int d = D.d_model, ffn = E->ffn;
+  auto& A = E->allocs;
+  int r = WXH_OK;
+  r = r ? r : dalloc(A, &E->conv1_w, (size_t)d * 3 * D.n_mels, true);
+  r = r ? r : dalloc(A, &E->conv2_w, (size_t)d * 3 * d, true);
+  r = r ? r : dalloc(A, &E->conv1_b, d, true);
+  r = r ? r : dalloc(A, &E->conv2_b, d, true);
+  r = r ? r : dalloc(A, &E->pos, (size_t)D.n_ctx * d, true);
+  r = r ? r : dalloc(A, &E->lnp_g, d, true);
+  r = r ? r : dalloc(A, &E->lnp_b, d, true);
+  E->layers.resize(D.n_layer);
+  for (auto& W : E->layers) {
+    r = r ? r : dalloc(A, &W.wqkv, (size_t)3 * d * d, true);
+    r = r ? r : dalloc(A, &W.wo, (size_t)d * d, true);
+    r = r ? r : dalloc(A, &W.w1, (size_t)ffn * d, true);
+    r = r ? r : dalloc(A, &W.w2, (size_t)d * ffn, true);
+    r = r ? r : dalloc(A, &W.bqkv, 3 * d, true);
+    r = r ? r : dalloc(A, &W.bo, d, true);
+    r = r ? r : dalloc(A, &W.b1, ffn, true);
+    r = r ? r : dalloc(A, &W.b2, d, true);
+    r = r ? r : dalloc(A, &W.ln1_g, d, true);
+    r = r ? r : dalloc(A, &W.ln1_b, d, true);
+    r = r ? r : dalloc(A, &W.ln2_g, d, true);
+    r = r ? r : dalloc(A, &W.ln2_b, d, true);
+  }
+  if (r != WXH_OK) {
+    free_list(E->allocs);
+    delete E;
+    return r;
+  }
+  *out = E;
+  return WXH_OK;
+}
+
+int wxh_encoder_destroy(wxh_encoder* E) {
+  if (!E) return WXH_OK;
+  (void)hipSetDevice(E->ctx->device);
+  (void)hipStreamSynchronize(E->ctx->stream);
+  drop_graphs(E);
+  free_list(E->ws_allocs);
+  free_list(E->allocs);
+  if (E->stage) (void)hipFree(E->stage);
+  delete E;
+  return WXH_OK;
+}
+
+int wxh_encoder_set_weight(wxh_encoder* E, const char* name, const float* host,
+                           const int64_t* shape, int ndim) {
+  WXH_REQUIRE(E && name && host && shape, "wxh_encoder_set_weight: null argument");
+  if (int r = check_ctx(E->ctx, 0, "wxh_encoder_set_weight")) return r;
+  std::string n = name;
+  if (n.rfind("w.", 0) == 0) n = n.substr(2);
+  const auto& D = E->dims;
+  const int64_t d = D.d_model, ffn = E->ffn, C = D.n_mels;
+  auto bad_shape = [&]() {
+    return fail(WXH_ERR_INVALID, "wxh_encoder_set_weight: %s has the wrong shape", name);
+  };
+  int r = WXH_OK;
+  if (n == "conv1.weight" || n == "conv2.weight") {
+    const int64_t cin = n == "conv1.weight" ? C : d;
+    if (!shape_is(shape, ndim, {d, cin, 3})) return bad_shape();
+    // (O, C, 3) -> [O][j*C + c]: tap-major K so a window of 3 rows is contiguous
+    std::vector<float> perm((size_t)d * 3 * cin);
+    for (int64_t o = 0; o < d; ++o)
+      for (int64_t c = 0; c < cin; ++c)
+        for (int64_t j = 0; j < 3; ++j)
+          perm[(size_t)o * 3 * cin + j * cin + c] = host[(o * cin + c) * 3 + j];
+    r = upload_bf16(E, n == "conv1.weight" ? E->conv1_w : E->conv2_w, perm.data(),
+                    (int)d, (int)(3 * cin));
+  } else if (n == "conv1.bias" || n == "conv2.bias" || n == "ln_post.weight" ||
+             n == "ln_post.bias") {
+    if (!shape_is(shape, ndim, {d})) return bad_shape();
+    float* dst = n == "conv1.bias" ? E->conv1_b
+                 : n == "conv2.bias" ? E->conv2_b
+                 : n == "ln_post.weight" ? E->lnp_g
+                                         : E->lnp_b;
+    r = upload_f32(E, dst, host, d);
+  } else if (n == "positional_embedding") {
+    if (!shape_is(shape, ndim, {D.n_ctx, d})) return bad_shape();
+    r = upload_f32(E, E->pos, host, (size_t)D.n_ctx * d);
+  } else if (n.rfind("blocks.", 0) == 0) {
+    const size_t dot = n.find('.', 7);
+    if (dot == std::string::npos) return fail(WXH_ERR_INVALID, "bad name %s", name);
+    const int L = std::atoi(n.substr(7, dot - 7).c_str());
+    if (L < 0 || L >= D.n_layer)
+      return fail(WXH_ERR_INVALID, "wxh_encoder_set_weight: %s: layer out of range", name);
+    const std::string t = n.substr(dot + 1);
+    LayerW& W = E->layers[L];
+    if (t == "attn.query.weight" || t == "attn.key.weight" || t == "attn.value.weight") {
+      if (!shape_is(shape, ndim, {d, d})) return bad_shape();
+      const int part = t == "attn.query.weight" ? 0 : t == "attn.key.weight" ? 1 : 2;
+      r = upload_bf16(E, W.wqkv + (size_t)part * d * d, host, (int)d, (int)d);
+    } else if (t == "attn.query.bias" || t == "attn.value.bias") {
+      if (!shape_is(shape, ndim, {d})) return bad_shape();
+      r = upload_f32(E, W.bqkv + (t == "attn.query.bias" ? 0 : 2 * d), host, d);
+    } else if (t == "attn.out.weight") {
+      if (!shape_is(shape, ndim, {d, d})) return bad_shape();
+      r = upload_bf16(E, W.wo, host, (int)d, (int)d);
+    } else if (t == "mlp.0.weight") {
+      if (!shape_is(shape, ndim, {ffn, d})) return bad_shape();
+      r = upload_bf16(E, W.w1, host, (int)ffn, (int)d);
+    } else if (t == "mlp.2.weight") {
+      if (!shape_is(shape, ndim, {d, ffn})) return bad_shape();
+      r = upload_bf16(E, W.w2, host, (int)d, (int)ffn);
+    } else if (t == "mlp.0.bias") {
+      if (!shape_is(shape, ndim, {ffn})) return bad_shape();
+      r = upload_f32(E, W.b1, host, ffn);
+    } else {
+      float* dst = t == "attn.out.bias"    ? W.bo
+                   : t == "mlp.2.bias"     ? W.b2
+                   : t == "attn_ln.weight" ? W.ln1_g
+                   : t == "attn_ln.bias"   ? W.ln1_b
+                   : t == "mlp_ln.weight"  ? W.ln2_g
+                   : t == "mlp_ln.bias"    ? W.ln2_b
+                                           : nullptr;
+      if (!dst) return fail(WXH_ERR_INVALID, "wxh_encoder_set_weight: unknown name %s", name);
+      if (!shape_is(shape, ndim, {d})) return bad_shape();
+      r = upload_f32(E, dst, host, d);
+    }
+  } else {
+    return fail(WXH_ERR_INVALID, "wxh_encoder_set_weight: unknown name %s", name);
+  }
+  if (r == WXH_OK) E->have[n] = true;
+  return r;
+}
+
+int wxh_encoder_ready(wxh_encoder* E) {
+  WXH_REQUIRE(E, "wxh_encoder_ready: null handle");
+  for (const auto& n : required_names(E->dims))
+    if (!E->have.count(n))
+      return fail(WXH_ERR_STATE, "encoder: weight %s has not been set", n.c_str());
+  return WXH_OK;
+}
+
+int wxh_encoder_set_graph(wxh_encoder* E, int enabled) {
+  WXH_REQUIRE(E, "wxh_encoder_set_graph: null handle");
+  E->use_graph = enabled != 0;
+  return WXH_OK;
+}
+
+int wxh_encoder_forward(wxh_encoder* E, const float* mel, int batch, int frames,
+                        float* out, void* stream) {
+  if (int r = check_forward_args(E, batch, frames)) return r;
+  WXH_REQUIRE(mel && out, "wxh_encoder_forward: null mel/out");
+  return forward_impl(E, mel, batch, frames, out, pick(E->ctx, stream), nullptr);
+}
+
+int wxh_encoder_forward_host(wxh_encoder* E, const float* mel_host, int batch,
+                             int frames, float* out_host) {
+  if (int r = check_forward_args(E, batch, frames)) return r;
+  WXH_REQUIRE(mel_host && out_host, "wxh_encoder_forward_host: null buffer");
+  const auto& D = E->dims;
+  const int ctx = (frames - 1) / 2 + 1;
+  const size_t n_in = (size_t)batch * D.n_mels * frames;
+  const size_t n_out = (size_t)batch * ctx * D.d_model;
+  float *dm = nullptr, *dout = nullptr;
+  WXH_HIP(hipMalloc(&dm, n_in * sizeof(float)));
+  hipError_t e = hipMalloc(&dout, n_out * sizeof(float));
+  if (e != hipSuccess) {
+    (void)hipFree(dm);
+    return fail(WXH_ERR_HIP, "hipMalloc: %s", hipGetErrorString(e));
+  }
+  hipStream_t s = E->ctx->stream;
+  int r = WXH_OK;
+  e = hipMemcpyAsync(dm, mel_host, n_in * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) r = fail(WXH_ERR_HIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
+  if (r == WXH_OK) r = forward_impl(E, dm, batch, frames, dout, s, nullptr);
+  if (r == WXH_OK) {
+    e = hipMemcpyAsync(out_host, dout, n_out * sizeof(float), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) r = fail(WXH_ERR_HIP, "copy out: %s", hipGetErrorString(e));
+  } else {
+    (void)hipStreamSynchronize(s);
+  }
+  (void)hipFree(dm);
+  (void)hipFree(dout);
+  return r;
+}
+
+int wxh_encoder_profile(wxh_encoder* E, const float* mel, int batch, int frames,
+                        float* out, float* ms, int n) {
+  if (int r = check_forward_args(E, batch, frames)) return r;
+  WXH_REQUIRE(mel && out && ms && n >= 0, "wxh_encoder_profile: null argument");
+  hipStream_t s = E->ctx->stream;
+  StageTimer t;
+  WXH_HIP(hipEventCreate(&t.start));
+  WXH_HIP(hipEventRecord(t.start, s));
+  int r = forward_impl(E, mel, batch, frames, out, s, &t);
+  hipError_t e = hipStreamSynchronize(s);
+  std::vector<float> acc(ST_COUNT, 0.f);
+  hipEvent_t prev = t.start;
+  for (auto& m : t.marks) {
+    float dt = 0.f;
+    if (r == WXH_OK && e == hipSuccess) (void)hipEventElapsedTime(&dt, prev, m.second);
+    acc[m.first] += dt;
+    prev = m.second;
+  }
+  for (auto& m : t.marks) (void)hipEventDestroy(m.second);
+  (void)hipEventDestroy(t.start);
+  if (r != WXH_OK) return r;
+  if (e != hipSuccess) return fail(WXH_ERR_HIP, "profile sync: %s", hipGetErrorString(e));
+  for (int i = 0; i < n; ++i) ms[i] = i < ST_COUNT ? acc[i] : 0.f;
+  return WXH_OK;
+}
+
+}  // extern "C"

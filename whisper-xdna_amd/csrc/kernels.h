@@ -1,0 +1,109 @@
+// Internal launch interface between the kernel files and the C-ABI / encoder.
+// Every function validates nothing: callers (capi.cpp, encoder.cpp) check
+// shapes, alignment and pointers first, so a launch here always fits the
+// kernel's assumptions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wx {
+
+enum DType { DT_BF16 = 0, DT_F32 = 1 };
+enum Gelu { GELU_NONE = -1, GELU_ERF = 0, GELU_POLY4_RNE = 1, GELU_POLY4_TRUNC = 2 };
+
+// ---------------------------------------------------------------- row ops
+// y = LN(x [+ resid]) * gamma + beta over each row of `cols` elements.
+// sum_out (fp32, optional) receives x + resid before normalisation.
+hipError_t launch_layernorm(const void* x, int x_dtype, int64_t ldx,
+                            const float* resid, int64_t ldr, float* sum_out,
+                            int64_t lds, const float* gamma, const float* beta,
+                            float eps, void* y, int y_dtype, int64_t ldy,
+                            int rows, int cols, hipStream_t s);
+
+// Max row width the one-wave-per-row LayerNorm and softmax keep in registers.
+constexpr int kMaxRowCols = 4096;
+
+// Element-wise GELU over a rows x cols band; y is bf16.
+hipError_t launch_gelu(const void* x, int x_dtype, int64_t ldx, uint16_t* y,
+                       int64_t ldy, int rows, int cols, int variant,
+                       hipStream_t s);
+
+// Row softmax over the first `valid` columns of bf16 rows (fp32 internals).
+hipError_t launch_softmax(const uint16_t* x, int64_t ldx, uint16_t* y,
+                          int64_t ldy, int rows, int valid, hipStream_t s);
+
+// fp32 [rows, cols] (ld ldx) -> bf16 RNE; transpose writes y[c*ldy + r].
+hipError_t launch_convert(const float* x, int64_t ldx, uint16_t* y,
+                          int64_t ldy, int rows, int cols, bool transpose,
+                          hipStream_t s);
+
+// ---------------------------------------------------------------- GEMM
+// C[M,N] = A[M,K] . W[N,K]^T with an epilogue. A row m lives at
+//   A + (m / a_rows_per_batch) * a_batch_stride + (m % a_rows_per_batch) * lda
+// which covers plain row-major A (a_rows_per_batch = M) and the conv
+// front-end's overlapping windows (lda = stride * channels).
+enum EpiMode {
+  EPI_F32 = 0,     // out fp32 = acc + bias
+  EPI_BF16 = 1,    // out bf16 = gelu?(acc + bias)
+  EPI_RESID = 2,   // resid fp32 += acc + bias
+  EPI_CONV1 = 3,   // padded bf16 out row (t + 1) of batch b = gelu_erf(acc + bias)
+  EPI_CONV2 = 4,   // resid fp32 = gelu_erf(acc + bias) + aux[t, n]
+  EPI_QKV = 5,     // split into head-major Q, K and transposed V (bf16)
+};
+
+struct GemmA {
+  const uint16_t* ptr;
+  int64_t lda;
+  int rows_per_batch;
+  int64_t batch_stride;
+};
+
+struct EpiParams {
+  void* out = nullptr;
+  int64_t ldo = 0;
+  const float* bias = nullptr;
+  const float* aux = nullptr;      // positional embedding [T, N] (EPI_CONV2)
+  int rows_per_batch = 1;          // T: rows of one batch item
+  int64_t out_batch_stride = 0;    // EPI_CONV1: elements per padded batch item
+  int gelu = GELU_NONE;            // EPI_BF16 activation
+  uint16_t* q = nullptr;           // EPI_QKV destinations
+  uint16_t* k = nullptr;
+  uint16_t* vt = nullptr;
+  int n_head = 0;
+  int t_pad = 0;                   // padded key length of Q/K/Vt
+  int d_model = 0;
+};
+
+hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
+                       int64_t ldw, int mode, const EpiParams& e,
+                       hipStream_t s);
+
+// ---------------------------------------------------------------- attention
+// Head dimension is fixed at 64 (Whisper: n_head = d_model / 64).
+constexpr int kHeadDim = 64;
+constexpr int kAttnKeyBlock = 64;
+inline int attn_padded_len(int T) {
+  return (T + kAttnKeyBlock - 1) / kAttnKeyBlock * kAttnKeyBlock;
+}
+
+// Q, K: [B*nh, Tp, 64] bf16; Vt: [B*nh, 64, Tp] bf16 (Tp = padded T, pads
+// finite). O row (b*T + t), column h*64 + j; bf16 or fp32 per o_dtype.
+hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
+                            const uint16_t* Vt, int batch, int n_head, int T,
+                            float scale, void* O, int o_dtype, int64_t ldo,
+                            hipStream_t s);
+
+// fp32 q, k, v rows [B*T, nh*64] (ld ld) -> the attention operand layouts.
+hipError_t launch_pack_qkv(const float* q, const float* k, const float* v,
+                           int64_t ld, int batch, int T, int n_head,
+                           uint16_t* Q, uint16_t* K, uint16_t* Vt,
+                           hipStream_t s);
+
+// ---------------------------------------------------------------- encoder
+// mel fp32 [B, C, T] -> bf16 [B, T + 2, C] with zero rows 0 and T + 1: the
+// conv1 im2col becomes a window of 3 consecutive rows.
+hipError_t launch_prep_mel(const float* mel, int batch, int C, int T,
+                           uint16_t* out, hipStream_t s);
+
+}  // namespace wx
