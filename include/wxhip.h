@@ -11,7 +11,8 @@
  *    wxh_last_error() returns a thread-local message. Nothing here aborts.
  *  - bf16 tensors are uint16_t bit patterns; fp32 tensors are float.
  *  - Pointers are DEVICE pointers unless the name says host. `stream` is a
- *    hipStream_t; NULL means the context's own stream. Calls are
+ *    hipStream_t; NULL is HIP's default (null) stream, as everywhere in the
+ *    HIP API (the context's own stream comes from wxh_get_stream). Calls are
  *    stream-ordered and asynchronous unless documented as synchronous.
  *  - One context is used by one host thread at a time (the reference RawRT is
  *    not thread-safe either; serve serialises it, npu_stt_server.py:131).

@@ -51,3 +51,13 @@ def cosine(a, b):
 def case(msg):
     """Name the case before a GPU step, flushed, so a crash log shows it."""
     print(f"[case] {msg}", flush=True)
+
+
+def report(name, **values):
+    """Append one JSON line of measured values to $WXH_REPORT when it is set
+    (the GPU runs collect cosines and error levels this way)."""
+    import json
+    path = os.environ.get("WXH_REPORT")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps({"case": name, **values}) + "\n")

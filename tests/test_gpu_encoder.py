@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import case, cosine
+from conftest import case, cosine, report
 from oracle import encoder as OE
 from wxhip import _lib as L
 from wxhip import synth
@@ -44,7 +44,7 @@ def test_tiny_encoder_cosine(dev, tiny):
     got = _fwd(_enc(dev, tiny), mel, dev)
     ref = OE.encoder_torch(tiny, mel)
     c = cosine(got, ref)
-    print(f"tiny cosine {c:.8f} max|d| {np.abs(got - ref).max():.4g}")
+    report("tiny_encoder", cosine=c, max_abs=float(np.abs(got - ref).max()))
     assert got.shape == (1500, 384) and np.isfinite(got).all()
     assert c >= 0.9999
 
@@ -55,7 +55,9 @@ def test_tiny_encoder_poly4_mlp(dev, tiny):
     case("encoder tiny poly4 MLP")
     mel = synth.make_mel(80, 3000, seed=1)
     got = _fwd(_enc(dev, tiny, mlp_gelu="poly4"), mel, dev)
-    assert cosine(got, OE.encoder_torch(tiny, mel)) >= 0.999
+    c = cosine(got, OE.encoder_torch(tiny, mel))
+    report("tiny_encoder_poly4_mlp", cosine=c)
+    assert c >= 0.999
 
 
 def test_batch_items_independent_and_graph_replay(dev, tiny):
@@ -79,7 +81,9 @@ def test_reduced_context_512(dev, tiny):
     mel = synth.make_mel(80, 1024, seed=2)
     got = _fwd(_enc(dev, tiny), mel, dev)
     assert got.shape == (512, 384)
-    assert cosine(got, OE.encoder_torch(tiny, mel)) >= 0.9999
+    c = cosine(got, OE.encoder_torch(tiny, mel))
+    report("tiny_encoder_ctx512", cosine=c)
+    assert c >= 0.9999
 
 
 def test_small_encoder_cosine(dev):
@@ -88,7 +92,7 @@ def test_small_encoder_cosine(dev):
     mel = synth.make_mel(80, 3000, seed=0)
     got = _fwd(_enc(dev, W), mel, dev)
     c = cosine(got, OE.encoder_torch(W, mel))
-    print(f"small cosine {c:.8f}")
+    report("small_encoder", cosine=c)
     assert c >= 0.9999
 
 
@@ -99,7 +103,7 @@ def test_large_v3_encoder_cosine(dev):
     got = _fwd(_enc(dev, W), mel, dev)
     ref = OE.encoder_torch(W, mel)
     c = cosine(got, ref)
-    print(f"large-v3 cosine {c:.8f}")
+    report("large_v3_encoder", cosine=c, max_abs=float(np.abs(got - ref).max()))
     assert got.shape == (1500, 1280) and np.isfinite(got).all()
     assert c >= 0.994
 

@@ -62,9 +62,9 @@ struct wxh_ctx {
 
 namespace {
 
-hipStream_t pick(wxh_ctx* c, void* s) {
-  return s ? static_cast<hipStream_t>(s) : c->stream;
-}
+// NULL is HIP's default (null) stream, exactly as in the HIP API; the
+// context's own stream is available through wxh_get_stream().
+hipStream_t pick(wxh_ctx*, void* s) { return static_cast<hipStream_t>(s); }
 
 int check_ctx(wxh_ctx* c, uint32_t bit, const char* what) {
   if (!c) return fail(WXH_ERR_INVALID, "%s: null context", what);

@@ -21,6 +21,12 @@ def _ptr(t):
     return C.c_void_p(t.data_ptr()) if t is not None else None
 
 
+def _ld(t):
+    """Row stride of a 2-D tensor; a single row's stride is meaningless (numpy
+    and torch may report 0), so it is taken as the row length."""
+    return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
+
+
 class Device:
     """One libwxhip context on GPU `index` (gfx950 only)."""
 
@@ -96,10 +102,10 @@ class Device:
             self._check(resid, torch.float32, "resid", 2)
         if sum_out is not None:
             self._check(sum_out, torch.float32, "sum_out", 2)
-        L.call("wxh_layernorm", self._h, _ptr(x), self._dt(x), x.stride(0),
-               _ptr(resid), resid.stride(0) if resid is not None else 0,
-               _ptr(sum_out), sum_out.stride(0) if sum_out is not None else 0,
-               _ptr(gamma), _ptr(beta), eps, _ptr(y), self._dt(y), y.stride(0),
+        L.call("wxh_layernorm", self._h, _ptr(x), self._dt(x), _ld(x),
+               _ptr(resid), _ld(resid) if resid is not None else 0,
+               _ptr(sum_out), _ld(sum_out) if sum_out is not None else 0,
+               _ptr(gamma), _ptr(beta), eps, _ptr(y), self._dt(y), _ld(y),
                rows, cols, self.stream())
         return y
 
@@ -112,8 +118,8 @@ class Device:
         self._check(y, torch.bfloat16, "out", 2)
         if tuple(y.shape[:1]) != (rows,) or y.shape[1] < cols:
             raise ValueError("out must have the rows of x and at least its columns")
-        L.call("wxh_gelu", self._h, _ptr(x), self._dt(x), x.stride(0), _ptr(y),
-               y.stride(0), rows, cols, variant, self.stream())
+        L.call("wxh_gelu", self._h, _ptr(x), self._dt(x), _ld(x), _ptr(y),
+               _ld(y), rows, cols, variant, self.stream())
         return y
 
     def softmax_rows(self, x, valid=None, out=None):
@@ -126,8 +132,8 @@ class Device:
             raise ValueError(f"valid={valid} outside (0, {cols}]")
         y = out if out is not None else torch.empty_like(x)
         self._check(y, torch.bfloat16, "out", 2)
-        L.call("wxh_softmax_rows", self._h, _ptr(x), x.stride(0), _ptr(y),
-               y.stride(0), rows, valid, self.stream())
+        L.call("wxh_softmax_rows", self._h, _ptr(x), _ld(x), _ptr(y),
+               _ld(y), rows, valid, self.stream())
         return y
 
     def to_bf16(self, x, transpose=False, out=None):
@@ -137,8 +143,8 @@ class Device:
         rows, cols = x.shape
         shape = (cols, rows) if transpose else (rows, cols)
         y = out if out is not None else torch.empty(shape, dtype=torch.bfloat16, device=self.device)
-        L.call("wxh_convert_f32_bf16", self._h, _ptr(x), x.stride(0), _ptr(y),
-               y.stride(0), rows, cols, int(transpose), self.stream())
+        L.call("wxh_convert_f32_bf16", self._h, _ptr(x), _ld(x), _ptr(y),
+               _ld(y), rows, cols, int(transpose), self.stream())
         return y
 
     # -- GEMM ------------------------------------------------------------------
@@ -164,8 +170,8 @@ class Device:
         self._check(out, odt, "out", 2)
         if tuple(out.shape) != (M, N):
             raise ValueError(f"out must be {(M, N)}")
-        L.call("wxh_gemm_bf16", self._h, M, N, K, _ptr(A), A.stride(0), _ptr(W),
-               W.stride(0), _ptr(bias), _ptr(out), out.stride(0), epilogue, self.stream())
+        L.call("wxh_gemm_bf16", self._h, M, N, K, _ptr(A), _ld(A), _ptr(W),
+               _ld(W), _ptr(bias), _ptr(out), _ld(out), epilogue, self.stream())
         return out
 
     # -- attention -------------------------------------------------------------
@@ -187,10 +193,10 @@ class Device:
             self._check(t, torch.float32, n, 2)
             if tuple(t.shape) != (batch * T, n_head * 64):
                 raise ValueError(f"{n} must be {(batch * T, n_head * 64)}")
-        if not (q.stride(0) == k.stride(0) == v.stride(0)):
+        if not (_ld(q) == _ld(k) == _ld(v)):
             raise ValueError("q, k, v must share a row stride")
         Q, K, Vt = bufs if bufs is not None else self.attn_buffers(batch, n_head, T)
-        L.call("wxh_pack_qkv", self._h, _ptr(q), _ptr(k), _ptr(v), q.stride(0), batch, T,
+        L.call("wxh_pack_qkv", self._h, _ptr(q), _ptr(k), _ptr(v), _ld(q), batch, T,
                n_head, _ptr(Q), _ptr(K), _ptr(Vt), self.stream())
         return Q, K, Vt
 
@@ -207,5 +213,5 @@ class Device:
         o = out if out is not None else torch.empty(batch * T, n_head * 64, dtype=out_dtype,
                                                     device=self.device)
         L.call("wxh_attention", self._h, _ptr(Q), _ptr(K), _ptr(Vt), batch, n_head, T,
-               float(scale), _ptr(o), self._dt(o), o.stride(0), self.stream())
+               float(scale), _ptr(o), self._dt(o), _ld(o), self.stream())
         return o

@@ -48,6 +48,10 @@ def _torch():
     return torch
 
 
+def _pad8(k):
+    return (k + 7) // 8 * 8
+
+
 class HipRT:
     # ONE GELU op for rt.gelu, as the reference keeps one overlay
     # (rawxrt.py:409-434); g4r = poly4 with RNE.
@@ -94,7 +98,10 @@ class HipRT:
             return self._wdev[key]
         t0 = time.perf_counter()
         src = torch.from_numpy(np.ascontiguousarray(B, dtype=np.float32)).to(self.dev.device)
-        w = self.dev.to_bf16(src, transpose=True)
+        K, N = src.shape
+        # the GEMM wants K % 8 == 0: zero-pad K (A is padded the same way)
+        w = torch.zeros(N, _pad8(K), dtype=torch.bfloat16, device=self.dev.device)
+        self.dev.to_bf16(src, transpose=True, out=w[:, :K])
         if key is not None:
             self._wdev[key] = w
         _t("upload_B", time.perf_counter() - t0)
@@ -117,7 +124,12 @@ class HipRT:
         torch = _torch()
         t0 = time.perf_counter()
         src = torch.from_numpy(np.ascontiguousarray(A, dtype=np.float32)).to(self.dev.device)
-        a = self.dev.to_bf16(src)
+        M, K = src.shape
+        if K % 8:
+            a = torch.zeros(M, _pad8(K), dtype=torch.bfloat16, device=self.dev.device)
+            self.dev.to_bf16(src, out=a[:, :K])
+        else:
+            a = self.dev.to_bf16(src)
         _t("upload_A", time.perf_counter() - t0)
         return a
 
