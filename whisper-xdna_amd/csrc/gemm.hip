@@ -14,6 +14,10 @@
 //   C: lane l holds column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4
 // The epilogue is fused: bias, GELU, residual add, the conv front end's
 // padded output and positional embedding, and the QKV head split.
+#include <cstdlib>
+#include <string>
+#include <utility>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -59,60 +63,117 @@ struct Cfg {
   static constexpr int LDS_BYTES = 2 * (BM + BN) * LDK * 2;
 };
 
-// Store four consecutive rows m0..m0+3 of one column n.
-template <int MODE>
-__device__ __forceinline__ void epi_store4(const EpiParams& e, int m0, int n,
-                                           const float* v, int M, int N) {
-  if (n >= N) return;
-  const float bias = e.bias ? e.bias[n] : 0.f;
-  if (MODE == EPI_QKV) {
-    const int d = e.d_model;
-    const int which = n / d;
-    const int nn = n - which * d;
-    const int h = nn >> 6, dd = nn & 63;
-    const int T = e.rows_per_batch;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + j;
-      if (m >= M) break;
-      const int b = m / T, t = m - b * T;
-      const int64_t bh = (int64_t)b * e.n_head + h;
-      const uint16_t val = f2bf(v[j] + bias);
-      if (which == 0)
-        e.q[(bh * e.t_pad + t) * 64 + dd] = val;
-      else if (which == 1)
-        e.k[(bh * e.t_pad + t) * 64 + dd] = val;
-      else
-        e.vt[(bh * 64 + dd) * e.t_pad + t] = val;
+// Compile-time loop: f(std::integral_constant<int, i>) for i in [0, N). Keeps
+// every accumulator index a constant whatever the unroller decides, so the
+// accumulators never get dynamically indexed (which would spill them).
+template <class F, int... Is>
+__device__ __forceinline__ void sfor_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  sfor_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Write one wave's TM x TN grid of 32x32 accumulator blocks through the
+// epilogue. Block (i, j) covers rows row0 + 32 i .. and columns col0 + 32 j ..;
+// lane l holds column l % 32 and rows 8 g + 4 (l / 32) + r (g, r < 4). Row-
+// and column-dependent parts of each output address are computed once per
+// 4-row group and once per column, not per element.
+template <int MODE, int TM, int TN>
+__device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&acc)[TM][TN],
+                                           int M, int N, int row0, int col0, int lane) {
+  const int l32 = lane & 31, half = lane >> 5;
+  int64_t cofs[TN];
+  int which[TN];
+  float bias[TN];
+  bool cok[TN];
+  static_for<TN>([&](auto j) {
+    const int n = col0 + j * 32 + l32;
+    cok[j] = n < N;
+    const int nn = cok[j] ? n : N - 1;
+    bias[j] = e.bias ? e.bias[nn] : 0.f;
+    which[j] = 0;
+    cofs[j] = nn;
+    if (MODE == EPI_QKV) {
+      const int wh = nn / e.d_model;
+      const int c = nn - wh * e.d_model;
+      const int h = c >> 6, dd = c & 63;
+      which[j] = wh;
+      cofs[j] = wh < 2 ? (int64_t)h * e.t_pad * 64 + dd
+                       : (int64_t)h * 64 * e.t_pad + (int64_t)dd * e.t_pad;
     }
-    return;
-  }
+  });
+  static_for<TM>([&](auto i) {
+    static_for<4>([&](auto g) {
+      const int m0 = row0 + i * 32 + g * 8 + half * 4;
+      // rows m0..m0+3: batch item b and position t, one division per group
+      int64_t r0[4], r1[4];
+      int tt[4];
+      bool rok[4];
+      const int T = e.rows_per_batch;
+      int b = m0 / T, t = m0 - b * T;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + j;
-    if (m >= M) break;
-    float x = v[j] + bias;
-    if (MODE == EPI_F32) {
-      static_cast<float*>(e.out)[(int64_t)m * e.ldo + n] = x;
-    } else if (MODE == EPI_BF16) {
-      if (e.gelu == GELU_ERF) x = gelu_erf(x);
-      else if (e.gelu == GELU_POLY4_RNE) x = epi_poly4(x);
-      static_cast<uint16_t*>(e.out)[(int64_t)m * e.ldo + n] = f2bf(x);
-    } else if (MODE == EPI_RESID) {
-      float* r = static_cast<float*>(e.out) + (int64_t)m * e.ldo + n;
-      *r = *r + x;
-    } else if (MODE == EPI_CONV1) {
-      const int T = e.rows_per_batch;
-      const int b = m / T, t = m - b * T;
-      static_cast<uint16_t*>(e.out)[(int64_t)b * e.out_batch_stride +
-                                    (int64_t)(t + 1) * e.ldo + n] = f2bf(gelu_erf(x));
-    } else if (MODE == EPI_CONV2) {
-      const int T = e.rows_per_batch;
-      const int t = m % T;
-      static_cast<float*>(e.out)[(int64_t)m * e.ldo + n] =
-          gelu_erf(x) + e.aux[(int64_t)t * N + n];
-    }
-  }
+      for (int r = 0; r < 4; ++r) {
+        rok[r] = m0 + r < M;
+        tt[r] = t;
+        if (MODE == EPI_CONV1)
+          r0[r] = (int64_t)b * e.out_batch_stride + (int64_t)(t + 1) * e.ldo;
+        else if (MODE == EPI_QKV) {
+          r0[r] = ((int64_t)b * e.n_head * e.t_pad + t) * 64;
+          r1[r] = (int64_t)b * e.n_head * 64 * e.t_pad + t;
+        } else
+          r0[r] = (int64_t)(m0 + r) * e.ldo;
+        if (++t >= T) {
+          t -= T;
+          ++b;
+          while (t >= T) { t -= T; ++b; }
+        }
+      }
+      static_for<TN>([&](auto j) {
+        if (!cok[j]) return;
+        const f32x16& a = acc[i][j];
+        if (MODE == EPI_QKV && which[j] == 2) {
+          // transposed V: four consecutive keys of one dim are contiguous
+          const int64_t o = r1[0] + cofs[j];
+          if (rok[3] && tt[3] == tt[0] + 3 && (o & 3) == 0) {
+            const u32x2 pk = {f2bf2(a[g * 4 + 0] + bias[j], a[g * 4 + 1] + bias[j]),
+                              f2bf2(a[g * 4 + 2] + bias[j], a[g * 4 + 3] + bias[j])};
+            *reinterpret_cast<u32x2*>(e.vt + o) = pk;
+            return;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (!rok[r]) continue;
+          float x = a[g * 4 + r] + bias[j];
+          if (MODE == EPI_F32) {
+            static_cast<float*>(e.out)[r0[r] + cofs[j]] = x;
+          } else if (MODE == EPI_BF16) {
+            if (e.gelu == GELU_ERF) x = gelu_erf(x);
+            else if (e.gelu == GELU_POLY4_RNE) x = epi_poly4(x);
+            static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(x);
+          } else if (MODE == EPI_RESID) {
+            float* p = static_cast<float*>(e.out) + r0[r] + cofs[j];
+            *p = *p + x;
+          } else if (MODE == EPI_CONV1) {
+            static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(gelu_erf(x));
+          } else if (MODE == EPI_CONV2) {
+            static_cast<float*>(e.out)[r0[r] + cofs[j]] =
+                gelu_erf(x) + e.aux[(int64_t)tt[r] * N + cofs[j]];
+          } else {  // EPI_QKV
+            const uint16_t val = f2bf(x);
+            if (which[j] == 0)
+              e.q[r0[r] + cofs[j]] = val;
+            else if (which[j] == 1)
+              e.k[r0[r] + cofs[j]] = val;
+            else
+              e.vt[r1[r] + cofs[j]] = val;
+          }
+        }
+      });
+    });
+  });
 }
 
 template <class C, int MODE>
@@ -223,20 +284,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(int M, int N, int K,
     __syncthreads();
   }
 
-  // epilogue: C fragment rows 8*g + 4*(lane/32) + (0..3), column lane % 32
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      const int n = bn0 + wn * C::WTN + j * 32 + (lane & 31);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int m0 = bm0 + wm * C::WTM + i * 32 + g * 8 + (lane >> 5) * 4;
-        float v[4] = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1],
-                      acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]};
-        epi_store4<MODE>(e, m0, n, v, M, N);
-      }
-    }
+  store_tile<MODE, C::TM, C::TN>(e, acc, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
 }
 
 template <class C>
@@ -272,11 +320,237 @@ static hipError_t gemm_launch_cfg(int M, int N, int K, const GemmA& a,
 
 using Cfg128 = Cfg<128, 128, 64, 2, 2>;
 
+// ====================================================================
+// v2: operands DMA'd straight from global memory into LDS with
+// buffer_load_dwordx4 ... lds (no VGPR staging), so the next K tile streams
+// in while the matrix cores work on the current one. One such instruction
+// writes 64 lanes x 16 bytes = 1 KB of LDS contiguously (lane l at byte
+// 16*l), i.e. 8 tile rows of 128 bytes (BK = 64 bf16). Bank conflicts are
+// avoided by an XOR swizzle instead of padding: 16-byte chunk c of tile row r
+// sits in slot c ^ (r & 7); each lane fetches the logical chunk that belongs
+// in its slot, so eight rows read at one logical chunk hit eight distinct
+// slots. Requires K % 64 == 0.
+template <int BM_, int BN_, int WM_, int WN_>
+struct DCfg {
+  static constexpr int BM = BM_, BN = BN_, BK = 64, WM = WM_, WN = WN_;
+  static constexpr int NW = WM * WN, NT = NW * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int TM = WTM / 32, TN = WTN / 32;
+  static constexpr int ROWB = BK * 2;  // bytes per tile row
+  static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
+  static constexpr int A_INSTR = A_BYTES / 1024 / NW;  // DMA instructions per wave
+  static constexpr int B_INSTR = B_BYTES / 1024 / NW;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static_assert(A_INSTR * 1024 * NW == A_BYTES && B_INSTR * 1024 * NW == B_BYTES,
+                "every wave issues whole 1 KB DMA blocks");
+  static_assert(TM >= 1 && TN >= 1, "wave tile");
+};
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+// L2). Renumber so that consecutive tile ids run on the same XCD, then walk
+// tiles in groups of kGroupM row-tiles so one XCD's concurrent tiles share A
+// rows and W columns in its L2. Both maps are bijections of [0, total).
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ int xcd_remap(int pid, int total) {
+  const int per = (total + kXcds - 1) / kXcds;
+  int tall = total % kXcds;
+  if (tall == 0) tall = kXcds;
+  const int xcd = pid % kXcds, local = pid / kXcds;
+  return xcd < tall ? xcd * per + local
+                    : tall * per + (xcd - tall) * (per - 1) + local;
+}
+
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <class C, int MODE>
+__global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, GemmA a,
+                                                       const uint16_t* __restrict__ W,
+                                                       int64_t ldw, EpiParams e,
+                                                       int a_bytes, int w_bytes) {
+  // The buffer-resource builtins exist only for the device; the host pass
+  // needs nothing but this kernel's launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int wm = w / C::WN, wn = w % C::WN;
+  const int l32 = lane & 31, half = lane >> 5;
+
+  const int nm = (M + C::BM - 1) / C::BM, nn = (N + C::BN - 1) / C::BN;
+  const int pid = xcd_remap(blockIdx.x, nm * nn);
+  const int width = kGroupM * nn;
+  const int first_m = (pid / width) * kGroupM;
+  const int gsz = min(nm - first_m, kGroupM);
+  const int tm = first_m + (pid % width) % gsz;
+  const int tn = (pid % width) / gsz;
+  const int bm0 = tm * C::BM, bn0 = tn * C::BN;
+
+  const auto ra = __builtin_amdgcn_make_buffer_rsrc((void*)a.ptr, (short)0, a_bytes, 0x00020000);
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, w_bytes, 0x00020000);
+
+  // lane -> (row within an 8-row group, swizzled logical chunk it fetches)
+  const int lrow = lane >> 3;
+  const int lchunk = (lane & 7) ^ lrow;
+  uint32_t aoff[C::A_INSTR], boff[C::B_INSTR];
+#pragma unroll
+  for (int j = 0; j < C::A_INSTR; ++j) {
+    const int row = (w * C::A_INSTR + j) * 8 + lrow;
+    int m = bm0 + row;
+    m = m < M ? m : M - 1;
+    const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+    aoff[j] = (uint32_t)(((int64_t)b * a.batch_stride + (int64_t)t * a.lda + lchunk * 8) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < C::B_INSTR; ++j) {
+    const int row = (w * C::B_INSTR + j) * 8 + lrow;
+    int n = bn0 + row;
+    n = n < N ? n : N - 1;
+    boff[j] = (uint32_t)(((int64_t)n * ldw + lchunk * 8) * 2);
+  }
+  auto issue = [&](int kt, int buf) {
+    uint8_t* base = smem + buf * C::STAGE;
+    const int soff = kt * C::BK * 2;
+#pragma unroll
+    for (int j = 0; j < C::A_INSTR; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (lds_ptr_t)(base + (w * C::A_INSTR + j) * 1024), 16, aoff[j], soff, 0, 0);
+#pragma unroll
+    for (int j = 0; j < C::B_INSTR; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rw, (lds_ptr_t)(base + C::A_BYTES + (w * C::B_INSTR + j) * 1024), 16, boff[j],
+          soff, 0, 0);
+  };
+
+  f32x16 acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = K / C::BK;
+  const int sw = l32 & 7;  // the swizzle of every row this lane reads
+  const int arow = (wm * C::WTM + l32) * C::ROWB;
+  const int brow = (wn * C::WTN + l32) * C::ROWB;
+  bf16x8 af[2][C::TM], bfr[2][C::TN];
+  auto load_frags = [&](const uint8_t* As, const uint8_t* Bs, int kk, int slot_set) {
+    const int slot = ((kk * 2 + half) ^ sw) << 4;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+      af[slot_set][i] = *reinterpret_cast<const bf16x8*>(As + arow + i * 32 * C::ROWB + slot);
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+      bfr[slot_set][j] = *reinterpret_cast<const bf16x8*>(Bs + brow + j * 32 * C::ROWB + slot);
+  };
+  issue(0, 0);
+  wait_vmcnt0();
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const uint8_t* As = smem + cur * C::STAGE;
+    const uint8_t* Bs = As + C::A_BYTES;
+    load_frags(As, Bs, 0, 0);
+    if (kt + 1 < nk) issue(kt + 1, cur ^ 1);
+    static_for<C::BK / 16>([&](auto kk) {
+      constexpr int set = kk & 1;
+      // fragments of the next k-slice load while this slice's MFMAs run
+      if constexpr (kk + 1 < C::BK / 16) load_frags(As, Bs, kk + 1, set ^ 1);
+      static_for<C::TM>([&](auto i) {
+        static_for<C::TN>([&](auto j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], bfr[set][j],
+                                                              acc[i][j], 0, 0, 0);
+        });
+      });
+      if constexpr (kk + 1 < C::BK / 16) {
+        // interleave: one LDS read between every few MFMAs
+        constexpr int nread = C::TM + C::TN;
+        constexpr int per = (C::TM * C::TN + nread - 1) / nread;
+        static_for<nread>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, per, 0);  // MFMA
+        });
+      }
+    });
+    wait_vmcnt0();
+    __syncthreads();
+  }
+
+  store_tile<MODE, C::TM, C::TN>(e, acc, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
+#endif
+}
+
+template <class C>
+static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const uint16_t* W,
+                                  int64_t ldw, int mode, const EpiParams& e,
+                                  int a_bytes, int w_bytes, hipStream_t s) {
+  const int tiles = ((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
+  dim3 grid(tiles), block(C::NT);
+#define WX_DMA(MD)                                                                   \
+  case MD:                                                                           \
+    gemm_dma_kernel<C, MD><<<grid, block, 0, s>>>(M, N, K, a, W, ldw, e, a_bytes,   \
+                                                  w_bytes);                          \
+    break;
+  switch (mode) {
+    WX_DMA(EPI_F32) WX_DMA(EPI_BF16) WX_DMA(EPI_RESID) WX_DMA(EPI_CONV1)
+    WX_DMA(EPI_CONV2) WX_DMA(EPI_QKV)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef WX_DMA
+  return hipGetLastError();
+}
+
+// Byte extent of A that rows [0, M) can touch (the buffer descriptor's
+// range); the largest row offset is that of the last row of the last batch
+// item or of the first batch item's last row.
+static int64_t a_extent_bytes(int M, int K, const GemmA& a) {
+  auto off = [&](int m) {
+    const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+    return (int64_t)b * a.batch_stride + (int64_t)t * a.lda;
+  };
+  const int last_first = (M < a.rows_per_batch ? M : a.rows_per_batch) - 1;
+  int64_t hi = off(M - 1);
+  const int64_t h2 = off(last_first);
+  if (h2 > hi) hi = h2;
+  return (hi + K) * 2;
+}
+
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
                        int64_t ldw, int mode, const EpiParams& e,
                        hipStream_t s) {
   if (M <= 0 || N <= 0) return hipSuccess;
-  return gemm_launch_cfg<Cfg128>(M, N, K, a, W, ldw, mode, e, s);
+  const int64_t ab = a_extent_bytes(M, K, a);
+  const int64_t wb = ((int64_t)(N - 1) * ldw + K) * 2;
+  const bool dma = K > 0 && K % 64 == 0 && a.lda % 8 == 0 && ldw % 8 == 0 &&
+                   a.batch_stride % 8 == 0 && ((uintptr_t)a.ptr & 15) == 0 &&
+                   ((uintptr_t)W & 15) == 0 && ab < (1ll << 31) && wb < (1ll << 31);
+  // WXH_GEMM_TILE overrides the tile choice (tuning sweeps):
+  // v1 | 128x128 | 256x128 | 256x256 | 256x256w8
+  const char* force = getenv("WXH_GEMM_TILE");
+  const std::string f = force ? force : "";
+  if (!dma || f == "v1") return gemm_launch_cfg<Cfg128>(M, N, K, a, W, ldw, mode, e, s);
+  using T128 = DCfg<128, 128, 2, 2>;
+  using T256x128 = DCfg<256, 128, 2, 2>;
+  using T256 = DCfg<256, 256, 2, 2>;
+  using T256w8 = DCfg<256, 256, 2, 4>;
+  if (f == "128x128") return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  if (f == "256x128") return gemm_dma_launch<T256x128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  if (f == "256x256") return gemm_dma_launch<T256>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  if (f == "256x256w8") return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  // Measured on MI355X (encoder shapes, batch 16 and 1): the 8-wave 256x256
+  // tile wins for narrow N (1280: out-proj, fc2), the 128x128 tile for wide N
+  // and for batch 1, where 256x256 leaves most CUs idle.
+  const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+  if (big_tiles >= 256 && N <= 2048)
+    return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
 }
 
 }  // namespace wx
