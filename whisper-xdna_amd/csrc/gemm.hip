@@ -322,36 +322,47 @@ using Cfg128 = Cfg<128, 128, 64, 2, 2>;
 
 // ====================================================================
 // v2: operands DMA'd straight from global memory into LDS with
-// buffer_load_dwordx4 ... lds (no VGPR staging), so the next K tile streams
-// in while the matrix cores work on the current one. One such instruction
-// writes 64 lanes x 16 bytes = 1 KB of LDS contiguously (lane l at byte
-// 16*l), i.e. 8 tile rows of 128 bytes (BK = 64 bf16). Bank conflicts are
-// avoided by an XOR swizzle instead of padding: 16-byte chunk c of tile row r
-// sits in slot c ^ (r & 7); each lane fetches the logical chunk that belongs
-// in its slot, so eight rows read at one logical chunk hit eight distinct
-// slots. Requires K % 64 == 0.
-template <int BM_, int BN_, int WM_, int WN_>
+// buffer_load_dwordx4 ... lds (no VGPR staging), through an S-stage ring so
+// the tile S-1 K-steps ahead is already in flight while the matrix cores work
+// on the current one. One such instruction writes 64 lanes x 16 bytes = 1 KB
+// of LDS contiguously (lane l at byte 16*l): 1024 / (2*BK) tile rows.
+// gfx950's LDS has 64 banks of 4 bytes and serves a 16-byte read for 16
+// lanes per cycle, so the 16 rows those lanes read must land in 16 distinct
+// 16-byte bank units. A row of 2*BK bytes covers 2*BK/256 of the banks, so an
+// XOR swizzle keyed on the row bits above that puts 16-byte chunk c of row r
+// in slot c ^ ((r / RPW) % CPR) (RPW rows per 256-byte bank window, CPR
+// chunks per row); each DMA lane fetches the logical chunk that belongs in
+// its slot. Requires K % BK == 0.
+template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_>
 struct DCfg {
-  static constexpr int BM = BM_, BN = BN_, BK = 64, WM = WM_, WN = WN_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, S = STAGES_;
   static constexpr int NW = WM * WN, NT = NW * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int ROWB = BK * 2;  // bytes per tile row
+  static constexpr int ROWB = BK * 2;            // bytes per tile row
+  static constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
+  static constexpr int RPW = 256 / ROWB;         // rows per 256-byte bank window
+  static constexpr int RPI = 1024 / ROWB;        // rows per 1 KB DMA instruction
   static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
   static constexpr int A_INSTR = A_BYTES / 1024 / NW;  // DMA instructions per wave
   static constexpr int B_INSTR = B_BYTES / 1024 / NW;
+  static constexpr int IPS = A_INSTR + B_INSTR;        // per stage per wave
   static constexpr int STAGE = A_BYTES + B_BYTES;
+  static_assert(BK == 32 || BK == 64, "BK");
   static_assert(A_INSTR * 1024 * NW == A_BYTES && B_INSTR * 1024 * NW == B_BYTES,
                 "every wave issues whole 1 KB DMA blocks");
   static_assert(TM >= 1 && TN >= 1, "wave tile");
+  static_assert(S >= 2 && (S - 1) * IPS <= 63, "vmcnt immediate");
+  static_assert(S * STAGE <= 160 * 1024, "LDS");
 };
 
-// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
-// L2). Renumber so that consecutive tile ids run on the same XCD, then walk
-// tiles in groups of kGroupM row-tiles so one XCD's concurrent tiles share A
-// rows and W columns in its L2. Both maps are bijections of [0, total).
+// Tiles are walked in groups of kGroupM row-tiles (all column tiles of a
+// group before the next), so concurrently running workgroups share A rows and
+// W columns in L2 / the Infinity Cache. Renumbering tile ids so that
+// consecutive ones land on one XCD (xcd_remap, assuming round-robin dispatch)
+// measured slower on the encoder shapes, so it is not applied.
 constexpr int kXcds = 8;
-constexpr int kGroupM = 8;
+constexpr int kGroupM = 16;
 
 __device__ __forceinline__ int xcd_remap(int pid, int total) {
   const int per = (total + kXcds - 1) / kXcds;
@@ -362,19 +373,26 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
                     : tall * per + (xcd - tall) * (per - 1) + local;
 }
 
-__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4],
+// lgkmcnt[11:8]; the other two counters left at their maximum, i.e. not
+// waited on)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0xF70);
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <class C, int MODE>
 __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, GemmA a,
-                                                       const uint16_t* __restrict__ W,
-                                                       int64_t ldw, EpiParams e,
-                                                       int a_bytes, int w_bytes) {
+                                                         const uint16_t* __restrict__ W,
+                                                         int64_t ldw, EpiParams e,
+                                                         int a_bytes, int w_bytes) {
   // The buffer-resource builtins exist only for the device; the host pass
   // needs nothing but this kernel's launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::S * C::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -383,7 +401,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   const int l32 = lane & 31, half = lane >> 5;
 
   const int nm = (M + C::BM - 1) / C::BM, nn = (N + C::BN - 1) / C::BN;
-  const int pid = xcd_remap(blockIdx.x, nm * nn);
+  const int pid = blockIdx.x;
   const int width = kGroupM * nn;
   const int first_m = (pid / width) * kGroupM;
   const int gsz = min(nm - first_m, kGroupM);
@@ -394,13 +412,14 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   const auto ra = __builtin_amdgcn_make_buffer_rsrc((void*)a.ptr, (short)0, a_bytes, 0x00020000);
   const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, w_bytes, 0x00020000);
 
-  // lane -> (row within an 8-row group, swizzled logical chunk it fetches)
-  const int lrow = lane >> 3;
-  const int lchunk = (lane & 7) ^ lrow;
+  // lane -> tile row within its DMA block and the logical chunk that belongs
+  // in its slot (lane % CPR) under the swizzle
+  const int lrow = lane / C::CPR;
   uint32_t aoff[C::A_INSTR], boff[C::B_INSTR];
 #pragma unroll
   for (int j = 0; j < C::A_INSTR; ++j) {
-    const int row = (w * C::A_INSTR + j) * 8 + lrow;
+    const int row = (w * C::A_INSTR + j) * C::RPI + lrow;
+    const int lchunk = (lane % C::CPR) ^ ((row / C::RPW) % C::CPR);
     int m = bm0 + row;
     m = m < M ? m : M - 1;
     const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
@@ -408,13 +427,14 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   }
 #pragma unroll
   for (int j = 0; j < C::B_INSTR; ++j) {
-    const int row = (w * C::B_INSTR + j) * 8 + lrow;
+    const int row = (w * C::B_INSTR + j) * C::RPI + lrow;
+    const int lchunk = (lane % C::CPR) ^ ((row / C::RPW) % C::CPR);
     int n = bn0 + row;
     n = n < N ? n : N - 1;
     boff[j] = (uint32_t)(((int64_t)n * ldw + lchunk * 8) * 2);
   }
-  auto issue = [&](int kt, int buf) {
-    uint8_t* base = smem + buf * C::STAGE;
+  auto issue = [&](int kt) {
+    uint8_t* base = smem + (kt % C::S) * C::STAGE;
     const int soff = kt * C::BK * 2;
 #pragma unroll
     for (int j = 0; j < C::A_INSTR; ++j)
@@ -436,50 +456,68 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int nk = K / C::BK;
-  const int sw = l32 & 7;  // the swizzle of every row this lane reads
+  const int sw = (l32 / C::RPW) % C::CPR;  // the swizzle of every row this lane reads
   const int arow = (wm * C::WTM + l32) * C::ROWB;
   const int brow = (wn * C::WTN + l32) * C::ROWB;
+  constexpr int KS = C::BK / 16;  // MFMA k-slices per K-step
+  constexpr int NR = C::TM + C::TN, NM = C::TM * C::TN;
   bf16x8 af[2][C::TM], bfr[2][C::TN];
-  auto load_frags = [&](const uint8_t* As, const uint8_t* Bs, int kk, int slot_set) {
+  auto load_frags = [&](int stage, int kk, int set) {
+    const uint8_t* As = smem + (stage % C::S) * C::STAGE;
+    const uint8_t* Bs = As + C::A_BYTES;
     const int slot = ((kk * 2 + half) ^ sw) << 4;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
-      af[slot_set][i] = *reinterpret_cast<const bf16x8*>(As + arow + i * 32 * C::ROWB + slot);
+      af[set][i] = *reinterpret_cast<const bf16x8*>(As + arow + i * 32 * C::ROWB + slot);
 #pragma unroll
     for (int j = 0; j < C::TN; ++j)
-      bfr[slot_set][j] = *reinterpret_cast<const bf16x8*>(Bs + brow + j * 32 * C::ROWB + slot);
+      bfr[set][j] = *reinterpret_cast<const bf16x8*>(Bs + brow + j * 32 * C::ROWB + slot);
   };
-  issue(0, 0);
-  wait_vmcnt0();
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const uint8_t* As = smem + cur * C::STAGE;
-    const uint8_t* Bs = As + C::A_BYTES;
-    load_frags(As, Bs, 0, 0);
-    if (kt + 1 < nk) issue(kt + 1, cur ^ 1);
-    static_for<C::BK / 16>([&](auto kk) {
-      constexpr int set = kk & 1;
-      // fragments of the next k-slice load while this slice's MFMAs run
-      if constexpr (kk + 1 < C::BK / 16) load_frags(As, Bs, kk + 1, set ^ 1);
-      static_for<C::TM>([&](auto i) {
-        static_for<C::TN>([&](auto j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], bfr[set][j],
-                                                              acc[i][j], 0, 0, 0);
-        });
+  auto mfmas = [&](int set) {
+    static_for<C::TM>([&](auto i) {
+      static_for<C::TN>([&](auto j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], bfr[set][j],
+                                                            acc[i][j], 0, 0, 0);
       });
-      if constexpr (kk + 1 < C::BK / 16) {
-        // interleave: one LDS read between every few MFMAs
-        constexpr int nread = C::TM + C::TN;
-        constexpr int per = (C::TM * C::TN + nread - 1) / nread;
-        static_for<nread>([&](auto) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, per, 0);  // MFMA
-        });
-      }
     });
-    wait_vmcnt0();
+  };
+
+  // Pipeline. Slot (kt % S) holds K-step kt; the DMA for step kt + S is issued
+  // right after the barrier of step kt, into the slot step kt just vacated.
+  // Within a step, the fragments of k-slice kk+1 are read from LDS before the
+  // MFMAs of slice kk are issued (each pair fenced into its own scheduling
+  // region, so the reads cannot sink behind the MFMAs and share their
+  // registers). The barrier, the refill and the first reads of step kt+1 sit
+  // in the last slice, ahead of its MFMAs.
+#pragma unroll
+  for (int st = 0; st < C::S; ++st)
+    if (st < nk) issue(st);
+  if (C::S - 1 < nk)
+    wait_vmcnt<(C::S - 1) * C::IPS>();
+  else
+    wait_vmcnt<0>();
+  __syncthreads();
+  load_frags(0, 0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    static_for<KS - 1>([&](auto kk) {
+      load_frags(kt, kk + 1, (kk + 1) & 1);
+      mfmas(kk & 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);  // the reads first
+      __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);  // then the MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    // step kt+1 must have landed; issued so far are steps 0 .. kt+S-1, so the
+    // S-2 steps after kt+1 may remain in flight (all of them near the end)
+    if (kt + C::S - 1 < nk)
+      wait_vmcnt<(C::S - 2) * C::IPS>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's reads done
     __syncthreads();
+    if (kt + C::S < nk) issue(kt + C::S);
+    if (kt + 1 < nk) load_frags(kt + 1, 0, 0);
+    mfmas((KS - 1) & 1);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   store_tile<MODE, C::TM, C::TN>(e, acc, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
@@ -531,24 +569,40 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   const bool dma = K > 0 && K % 64 == 0 && a.lda % 8 == 0 && ldw % 8 == 0 &&
                    a.batch_stride % 8 == 0 && ((uintptr_t)a.ptr & 15) == 0 &&
                    ((uintptr_t)W & 15) == 0 && ab < (1ll << 31) && wb < (1ll << 31);
-  // WXH_GEMM_TILE overrides the tile choice (tuning sweeps):
-  // v1 | 128x128 | 256x128 | 256x256 | 256x256w8
+  // WXH_GEMM_TILE overrides the tile choice (tuning sweeps)
   const char* force = getenv("WXH_GEMM_TILE");
   const std::string f = force ? force : "";
   if (!dma || f == "v1") return gemm_launch_cfg<Cfg128>(M, N, K, a, W, ldw, mode, e, s);
-  using T128 = DCfg<128, 128, 2, 2>;
-  using T256x128 = DCfg<256, 128, 2, 2>;
-  using T256 = DCfg<256, 256, 2, 2>;
-  using T256w8 = DCfg<256, 256, 2, 4>;
-  if (f == "128x128") return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
-  if (f == "256x128") return gemm_dma_launch<T256x128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
-  if (f == "256x256") return gemm_dma_launch<T256>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
-  if (f == "256x256w8") return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
-  // Measured on MI355X (encoder shapes, batch 16 and 1): the 8-wave 256x256
-  // tile wins for narrow N (1280: out-proj, fc2), the 128x128 tile for wide N
-  // and for batch 1, where 256x256 leaves most CUs idle.
+  using T128 = DCfg<128, 128, 2, 2, 64, 2>;
+  using T128k32s4 = DCfg<128, 128, 2, 2, 32, 4>;
+  using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
+  using T256w8k32s4 = DCfg<256, 256, 2, 4, 32, 4>;
+  using T256x128w8k32s4 = DCfg<256, 128, 4, 2, 32, 4>;
+  using T256x128k64s2 = DCfg<256, 128, 2, 2, 64, 2>;
+  using T256w8k32s5 = DCfg<256, 256, 2, 4, 32, 5>;
+  using T128k32s6 = DCfg<128, 128, 2, 2, 32, 6>;
+  using T128k64s3 = DCfg<128, 128, 2, 2, 64, 3>;
+#define WX_TRY(NAME, CFG)                                                              \
+  if (f == NAME) {                                                                     \
+    if (K % CFG::BK) return hipErrorInvalidValue;                                      \
+    return gemm_dma_launch<CFG>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);     \
+  }
+  WX_TRY("128x128", T128)
+  WX_TRY("128x128k32s4", T128k32s4)
+  WX_TRY("256x256w8", T256w8)
+  WX_TRY("256x256w8k32s4", T256w8k32s4)
+  WX_TRY("256x128w8k32s4", T256x128w8k32s4)
+  WX_TRY("256x128", T256x128k64s2)
+  WX_TRY("256x256w8k32s5", T256w8k32s5)
+  WX_TRY("128x128k32s6", T128k32s6)
+  WX_TRY("128x128k64s3", T128k64s3)
+#undef WX_TRY
+  // Measured on MI355X over the encoder shapes with random operands: the
+  // 8-wave 256x256 tile (128x64 per wave, 2 waves per SIMD) is fastest once
+  // there are enough tiles to fill the 256 CUs (batch 16: 800-1050 TFLOP/s);
+  // below that (batch 1) the 128x128 tile keeps more CUs busy.
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-  if (big_tiles >= 256 && N <= 2048)
+  if (big_tiles >= 256)
     return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
 }
