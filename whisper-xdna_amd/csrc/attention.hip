@@ -14,8 +14,9 @@
 // which is the same function with one rounding less.
 //
 // Layout: Q, K [B*nh, Tp, 64] and Vt [B*nh, 64, Tp] bf16 (Tp = T rounded up
-// to 64, pad rows/columns finite). A workgroup owns 128 query rows of one
-// head (4 waves x 32 rows) and streams 64-key K/V tiles through LDS.
+// to 64, pad rows/columns finite; Vt keys placed by vt_key). A workgroup owns
+// 128 query rows of one head (4 waves x 32 rows) and streams 64-key K/Vt
+// tiles through a 3-stage LDS ring filled by direct-to-LDS loads.
 // Scores are computed transposed, S^T = K Q^T with v_mfma_f32_32x32x16_bf16,
 // so a lane owns one query column and 16 keys per 32-key block: the row max
 // and row sum are lane-local plus one exchange between the two lane halves,
@@ -27,17 +28,31 @@
 
 namespace wx {
 
-constexpr int kQB = 128;         // query rows per workgroup
+constexpr int kQB = 128;            // query rows per workgroup (4 waves x 32)
 constexpr int kKB = kAttnKeyBlock;  // keys per LDS tile
-constexpr int kLD = 72;          // padded LDS row (elements)
+constexpr int kStages = 3;          // K/Vt tiles in flight
+constexpr int kTile = kKB * 128;    // one 64 x 64 bf16 tile: 64 rows of 128 bytes
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0xF70);
+}
+
+// K tile [64 keys][64 dims] and Vt tile [64 dims][64 keys] stream through a
+// kStages-deep LDS ring by buffer_load_dwordx4 ... lds (1 KB = 8 rows per
+// instruction, lane l at byte 16 l). Rows are 128 bytes; 16-byte chunk c of
+// row r sits in slot c ^ ((r >> 1) & 7), which makes the 16-lane groups of a
+// ds_read_b128 hit 16 distinct bank units on gfx950's 64-bank LDS.
 template <bool OUT_F32>
 __global__ __launch_bounds__(256) void attn_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ Vt, int n_head, int T, int Tp,
     float scale_log2, void* __restrict__ O, int64_t ldo) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKB * kLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kHeadDim * kLD];
+#if defined(__HIP_DEVICE_COMPILE__)
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * 2 * kTile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -50,14 +65,37 @@ __global__ __launch_bounds__(256) void attn_kernel(
   const uint16_t* Qh = Q + bh * Tp * kHeadDim;
   const uint16_t* Kh = K + bh * Tp * kHeadDim;
   const uint16_t* Vh = Vt + bh * kHeadDim * Tp;
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, Tp * kHeadDim * 2, 0x00020000);
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vh, (short)0, kHeadDim * Tp * 2, 0x00020000);
+
+  // DMA: wave w moves tile rows 16 w .. 16 w + 15 of both tiles
+  const int lrow = lane >> 3;
+  uint32_t koff[2], voff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = (w * 2 + j) * 8 + lrow;
+    const int lchunk = (lane & 7) ^ ((row >> 1) & 7);
+    koff[j] = (uint32_t)((row * kHeadDim + lchunk * 8) * 2);
+    voff[j] = (uint32_t)((row * Tp + lchunk * 8) * 2);
+  }
+  auto issue = [&](int kb) {
+    uint8_t* base = smem + (kb % kStages) * 2 * kTile;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(base + (w * 2 + j) * 1024), 16,
+                                               koff[j], kb * kKB * kHeadDim * 2, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(base + kTile + (w * 2 + j) * 1024),
+                                               16, voff[j], kb * kKB * 2, 0, 0);
+  };
 
   int qrow = q0 + l32;
   qrow = qrow < Tp ? qrow : Tp - 1;
   bf16x8 qf[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk)
-    qf[kk] = *reinterpret_cast<const bf16x8*>(Qh + (int64_t)qrow * kHeadDim +
-                                              kk * 16 + half * 8);
+    qf[kk] = *reinterpret_cast<const bf16x8*>(Qh + (int64_t)qrow * kHeadDim + kk * 16 + half * 8);
 
   f32x16 o[2];
 #pragma unroll
@@ -65,34 +103,47 @@ __global__ __launch_bounds__(256) void attn_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+  const int sw = (l32 >> 1) & 7;  // the swizzle of every row this lane reads
 
   const int nkb = Tp / kKB;
-  for (int kb = 0; kb < nkb; ++kb) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * 256;
-      const int r = c >> 3, kc = (c & 7) * 8;
-      *reinterpret_cast<u32x4*>(&Ks[r * kLD + kc]) =
-          *reinterpret_cast<const u32x4*>(Kh + (int64_t)(kb * kKB + r) * kHeadDim + kc);
-      *reinterpret_cast<u32x4*>(&Vs[r * kLD + kc]) =
-          *reinterpret_cast<const u32x4*>(Vh + (int64_t)r * Tp + kb * kKB + kc);
-    }
-    __syncthreads();
+  for (int st = 0; st < kStages; ++st)
+    if (st < nkb) issue(st);
+  if (kStages - 1 < nkb)
+    wait_vm<(kStages - 1) * 4>();
+  else
+    wait_vm<0>();
+  __syncthreads();
 
-    // S^T for two 32-key blocks
+  for (int kb = 0; kb < nkb; ++kb) {
+    const uint8_t* Ks = smem + (kb % kStages) * 2 * kTile;
+    const uint8_t* Vs = Ks + kTile;
+    // all 16 fragments of the tile are read up front: the K reads feed the
+    // score MFMAs, the V reads land while the softmax runs
+    bf16x8 ka[2][4], va[4][2];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        ka[k2][kk] = *reinterpret_cast<const bf16x8*>(
+            Ks + (k2 * 32 + l32) * 128 + (((kk * 2 + half) ^ sw) << 4));
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+        va[ks][db] = *reinterpret_cast<const bf16x8*>(
+            Vs + (db * 32 + l32) * 128 + (((ks * 2 + half) ^ sw) << 4));
+    // S^T = K Q^T for two 32-key blocks
     f32x16 s[2];
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[k2][r] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(
-            &Ks[(k2 * 32 + l32) * kLD + kk * 16 + half * 8]);
-        s[k2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[kk], s[k2], 0, 0, 0);
-      }
+      for (int kk = 0; kk < 4; ++kk)
+        s[k2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[k2][kk], qf[kk], s[k2], 0, 0, 0);
     }
-    // scale (log2 domain), mask, block max
+    // scale (log2 domain), mask keys >= T, block max
     float mx = -INFINITY;
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2)
@@ -116,31 +167,33 @@ __global__ __launch_bounds__(256) void attn_kernel(
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float p0 = exp2f(s[k2][2 * j] - m_new);
-        const float p1 = exp2f(s[k2][2 * j + 1] - m_new);
+        const float p0 = __builtin_amdgcn_exp2f(s[k2][2 * j] - m_new);
+        const float p1 = __builtin_amdgcn_exp2f(s[k2][2 * j + 1] - m_new);
         l_run += p0 + p1;
         pk[k2][j] = f2bf2(p0, p1);
       }
     m_run = m_new;
 
-    // O^T += V^T P^T over the 64 keys of the tile, 16 keys per MFMA
+    // O^T += V^T P^T, 16 keys per MFMA; Vt rows hold each lane half's 8 keys
+    // contiguously (vt_key), so one 16-byte read is the whole A fragment
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int k2 = ks >> 1, sub = ks & 1;
-      const u32x4 pv = {pk[k2][4 * sub + 0], pk[k2][4 * sub + 1],
-                        pk[k2][4 * sub + 2], pk[k2][4 * sub + 3]};
+      const u32x4 pv = {pk[k2][4 * sub + 0], pk[k2][4 * sub + 1], pk[k2][4 * sub + 2],
+                        pk[k2][4 * sub + 3]};
       const bf16x8 pb = __builtin_bit_cast(bf16x8, pv);
 #pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const uint16_t* vrow = &Vs[(db * 32 + l32) * kLD + 16 * ks + 4 * half];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-        const u32x4 vv = {lo[0], lo[1], hi[0], hi[1]};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8, vv), pb, o[db], 0, 0, 0);
-      }
+      for (int db = 0; db < 2; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[ks][db], pb, o[db], 0, 0, 0);
     }
+    // tile kb+1 must have landed (the stages after it may still fly); every
+    // wave is done with slot kb once past the barrier, which it then refills
+    if (kb + kStages - 1 < nkb)
+      wait_vm<(kStages - 2) * 4>();
+    else
+      wait_vm<0>();
     __syncthreads();
+    if (kb + kStages < nkb) issue(kb + kStages);
   }
 
   l_run += __shfl_xor(l_run, 32, 64);
@@ -163,6 +216,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
         *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(O) + orow + d0) = vv;
       }
     }
+#endif
 }
 
 hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
@@ -195,7 +249,7 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(
     const int64_t bh = (int64_t)b * n_head + h;
     Qo[(bh * Tp + t) * kHeadDim + dd] = f2bf(q[src + n]);
     Ko[(bh * Tp + t) * kHeadDim + dd] = f2bf(k[src + n]);
-    Vo[(bh * kHeadDim + dd) * Tp + t] = f2bf(v[src + n]);
+    Vo[(bh * kHeadDim + dd) * Tp + vt_key(t)] = f2bf(v[src + n]);
   }
 }
 

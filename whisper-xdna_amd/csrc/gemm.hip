@@ -121,7 +121,7 @@ __device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&ac
           r0[r] = (int64_t)b * e.out_batch_stride + (int64_t)(t + 1) * e.ldo;
         else if (MODE == EPI_QKV) {
           r0[r] = ((int64_t)b * e.n_head * e.t_pad + t) * 64;
-          r1[r] = (int64_t)b * e.n_head * 64 * e.t_pad + t;
+          r1[r] = (int64_t)b * e.n_head * 64 * e.t_pad + vt_key(t);
         } else
           r0[r] = (int64_t)(m0 + r) * e.ldo;
         if (++t >= T) {
@@ -136,7 +136,7 @@ __device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&ac
         if (MODE == EPI_QKV && which[j] == 2) {
           // transposed V: four consecutive keys of one dim are contiguous
           const int64_t o = r1[0] + cofs[j];
-          if (rok[3] && tt[3] == tt[0] + 3 && (o & 3) == 0) {
+          if (rok[3] && tt[3] == tt[0] + 3 && (tt[0] & 3) == 0 && (o & 3) == 0) {
             const u32x2 pk = {f2bf2(a[g * 4 + 0] + bias[j], a[g * 4 + 1] + bias[j]),
                               f2bf2(a[g * 4 + 2] + bias[j], a[g * 4 + 3] + bias[j])};
             *reinterpret_cast<u32x2*>(e.vt + o) = pk;
@@ -150,17 +150,17 @@ __device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&ac
           if (MODE == EPI_F32) {
             static_cast<float*>(e.out)[r0[r] + cofs[j]] = x;
           } else if (MODE == EPI_BF16) {
-            if (e.gelu == GELU_ERF) x = gelu_erf(x);
+            if (e.gelu == GELU_ERF) x = gelu_erf_fast(x);
             else if (e.gelu == GELU_POLY4_RNE) x = epi_poly4(x);
             static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(x);
           } else if (MODE == EPI_RESID) {
             float* p = static_cast<float*>(e.out) + r0[r] + cofs[j];
             *p = *p + x;
           } else if (MODE == EPI_CONV1) {
-            static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(gelu_erf(x));
+            static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(gelu_erf_fast(x));
           } else if (MODE == EPI_CONV2) {
             static_cast<float*>(e.out)[r0[r] + cofs[j]] =
-                gelu_erf(x) + e.aux[(int64_t)tt[r] * N + cofs[j]];
+                gelu_erf_fast(x) + e.aux[(int64_t)tt[r] * N + cofs[j]];
           } else {  // EPI_QKV
             const uint16_t val = f2bf(x);
             if (which[j] == 0)

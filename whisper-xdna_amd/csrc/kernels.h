@@ -87,8 +87,17 @@ inline int attn_padded_len(int T) {
   return (T + kAttnKeyBlock - 1) / kAttnKeyBlock * kAttnKeyBlock;
 }
 
-// Q, K: [B*nh, Tp, 64] bf16; Vt: [B*nh, 64, Tp] bf16 (Tp = padded T, pads
-// finite). O row (b*T + t), column h*64 + j; bf16 or fp32 per o_dtype.
+// Position of key t in a row of Vt: within each group of 16 keys, the four
+// groups of 4 are stored in the order 0, 2, 1, 3, so the 8 keys one lane
+// half multiplies in the P.V MFMA (keys 4h..4h+3 and 8+4h..8+4h+3 of the
+// group) are 16 contiguous bytes. Groups of 4 stay contiguous.
+__host__ __device__ inline int vt_key(int t) {
+  return (t & ~15) | (((t >> 2) & 1) << 3) | (((t >> 3) & 1) << 2) | (t & 3);
+}
+
+// Q, K: [B*nh, Tp, 64] bf16; Vt: [B*nh, 64, Tp] bf16 with keys placed by
+// vt_key (Tp = padded T, pads finite). O row (b*T + t), column h*64 + j;
+// bf16 or fp32 per o_dtype.
 hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
                             const uint16_t* Vt, int batch, int n_head, int T,
                             float scale, void* O, int o_dtype, int64_t ldo,
