@@ -176,6 +176,106 @@ __device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&ac
   });
 }
 
+// The LDS-DMA kernels multiply with the operands swapped, C^T = W . A^T, so
+// that a lane's accumulator holds one ROW of C: block (i, j) covers row
+// row0 + 32 i + l % 32 and columns col0 + 32 j + 8 g + 4 (l / 32) + 0..3 for
+// g < 4. Each lane then writes four runs of 4 consecutive columns: 8-byte
+// (bf16) or 16-byte (fp32) stores and loads, one row's address math per
+// block row, and a read-modify-write of the fp32 residual in 16-byte pieces.
+// Column runs that cross N, or outputs whose row stride or base are not
+// aligned for the vector access, take the scalar path.
+template <int MODE, int TM, int TN>
+__device__ __forceinline__ void store_tile_t(const EpiParams& e, const f32x16 (&acc)[TM][TN],
+                                             int M, int N, int row0, int col0, int lane) {
+  const int l32 = lane & 31, half = lane >> 5;
+  const uintptr_t ob = (uintptr_t)e.out;
+  const bool v32 = (e.ldo & 3) == 0 && (ob & 15) == 0;  // fp32 runs are 16-byte aligned
+  const bool v16 = (e.ldo & 3) == 0 && (ob & 7) == 0;   // bf16 runs are 8-byte aligned
+  const bool vb = ((uintptr_t)e.bias & 15) == 0;
+  f32x4 bias[TN][4];
+  static_for<TN>([&](auto j) {
+    static_for<4>([&](auto g) {
+      const int n0 = col0 + j * 32 + g * 8 + half * 4;
+      if (e.bias && vb && n0 + 3 < N) {
+        bias[j][g] = *reinterpret_cast<const f32x4*>(e.bias + n0);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bias[j][g][r] = (e.bias && n0 + r < N) ? e.bias[n0 + r] : 0.f;
+      }
+    });
+  });
+  static_for<TM>([&](auto i) {
+    const int m = row0 + i * 32 + l32;
+    if (m >= M) return;
+    const int T = e.rows_per_batch;
+    const int b = m / T, t = m - b * T;
+    int64_t r0, r1 = 0;
+    if (MODE == EPI_CONV1) {
+      r0 = (int64_t)b * e.out_batch_stride + (int64_t)(t + 1) * e.ldo;
+    } else if (MODE == EPI_QKV) {
+      r0 = ((int64_t)b * e.n_head * e.t_pad + t) * 64;
+      r1 = (int64_t)b * e.n_head * 64 * e.t_pad + vt_key(t);
+    } else {
+      r0 = (int64_t)m * e.ldo;
+    }
+    static_for<TN>([&](auto j) {
+      static_for<4>([&](auto g) {
+        const int n0 = col0 + j * 32 + g * 8 + half * 4;
+        if (n0 >= N) return;
+        const bool full = n0 + 3 < N;
+        float x[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = acc[i][j][g * 4 + r] + bias[j][g][r];
+        if (MODE == EPI_F32 || MODE == EPI_RESID || MODE == EPI_CONV2) {
+          float* p = static_cast<float*>(e.out) + r0 + n0;
+          if (MODE == EPI_CONV2) {
+            const float* ap = e.aux + (int64_t)t * N + n0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[r] = gelu_erf_fast(x[r]) + (n0 + r < N ? ap[r] : 0.f);
+          }
+          if (full && v32) {
+            f32x4 v = {x[0], x[1], x[2], x[3]};
+            if (MODE == EPI_RESID) v += *reinterpret_cast<const f32x4*>(p);
+            *reinterpret_cast<f32x4*>(p) = v;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n0 + r < N) p[r] = MODE == EPI_RESID ? p[r] + x[r] : x[r];
+          }
+        } else if (MODE == EPI_BF16 || MODE == EPI_CONV1) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (MODE == EPI_CONV1 || e.gelu == GELU_ERF) x[r] = gelu_erf_fast(x[r]);
+            else if (e.gelu == GELU_POLY4_RNE) x[r] = epi_poly4(x[r]);
+          }
+          uint16_t* p = static_cast<uint16_t*>(e.out) + r0 + n0;
+          if (full && v16) {
+            const u32x2 v = {f2bf2(x[0], x[1]), f2bf2(x[2], x[3])};
+            *reinterpret_cast<u32x2*>(p) = v;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n0 + r < N) p[r] = f2bf(x[r]);
+          }
+        } else {  // EPI_QKV: d_model % 64 == 0, so a 4-run stays in one head
+          const int wh = n0 / e.d_model;
+          const int c = n0 - wh * e.d_model;
+          const int h = c >> 6, dd = c & 63;
+          if (wh < 2) {
+            uint16_t* p = (wh == 0 ? e.q : e.k) + r0 + (int64_t)h * e.t_pad * 64 + dd;
+            const u32x2 v = {f2bf2(x[0], x[1]), f2bf2(x[2], x[3])};
+            *reinterpret_cast<u32x2*>(p) = v;
+          } else {
+            uint16_t* p = e.vt + r1 + ((int64_t)h * 64 + dd) * e.t_pad;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) p[(int64_t)r * e.t_pad] = f2bf(x[r]);
+          }
+        }
+      });
+    });
+  });
+}
+
 template <class C, int MODE>
 __global__ __launch_bounds__(C::NT) void gemm_kernel(int M, int N, int K,
                                                      GemmA a,
@@ -476,7 +576,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   auto mfmas = [&](int set) {
     static_for<C::TM>([&](auto i) {
       static_for<C::TN>([&](auto j) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[set][i], bfr[set][j],
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[set][j], af[set][i],
                                                             acc[i][j], 0, 0, 0);
       });
     });
@@ -520,7 +620,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  store_tile<MODE, C::TM, C::TN>(e, acc, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
+  store_tile_t<MODE, C::TM, C::TN>(e, acc, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
 #endif
 }
 
@@ -582,6 +682,7 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   using T256w8k32s5 = DCfg<256, 256, 2, 4, 32, 5>;
   using T128k32s6 = DCfg<128, 128, 2, 2, 32, 6>;
   using T128k64s3 = DCfg<128, 128, 2, 2, 64, 3>;
+  using T256w4 = DCfg<256, 256, 2, 2, 64, 2>;
 #define WX_TRY(NAME, CFG)                                                              \
   if (f == NAME) {                                                                     \
     if (K % CFG::BK) return hipErrorInvalidValue;                                      \
@@ -596,13 +697,17 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   WX_TRY("256x256w8k32s5", T256w8k32s5)
   WX_TRY("128x128k32s6", T128k32s6)
   WX_TRY("128x128k64s3", T128k64s3)
+  WX_TRY("256x256w4", T256w4)
 #undef WX_TRY
   // Measured on MI355X over the encoder shapes with random operands: the
-  // 8-wave 256x256 tile (128x64 per wave, 2 waves per SIMD) is fastest once
-  // there are enough tiles to fill the 256 CUs (batch 16: 800-1050 TFLOP/s);
-  // below that (batch 1) the 128x128 tile keeps more CUs busy.
+  // 8-wave 256x256 tile (128x64 per wave, 2 waves per SIMD, one workgroup per
+  // CU) is fastest for the narrow outputs (N <= 2048: out-proj, fc2) once
+  // there are enough tiles to fill the 256 CUs. For wide outputs (fc1, QKV)
+  // the 128x128 tile wins: two workgroups share a CU, so one's epilogue (the
+  // GELU and the bf16 stores of a large output) overlaps the other's main
+  // loop. At batch 1 the 128x128 tile also keeps more CUs busy.
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-  if (big_tiles >= 256)
+  if (big_tiles >= 256 && N <= 2048)
     return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
 }
