@@ -143,20 +143,28 @@ __global__ __launch_bounds__(256) void attn_kernel(
       for (int kk = 0; kk < 4; ++kk)
         s[k2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[k2][kk], qf[kk], s[k2], 0, 0, 0);
     }
-    // scale (log2 domain), mask keys >= T, block max
+    // Keys >= T exist only in the last block: mask them there (a uniform
+    // branch), nowhere else. The running max is kept in raw score units and
+    // the scale enters once, in the FMA that forms the exp2 argument:
+    // p = 2^(s c - m c) with c = scale * log2(e), m the running max.
+    if ((kb + 1) * kKB > T) {
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb * kKB + k2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (key >= T) s[k2][r] = -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb * kKB + k2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        const float val = key < T ? s[k2][r] * scale_log2 : -INFINITY;
-        s[k2][r] = val;
-        mx = fmaxf(mx, val);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[k2][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+    const float mc = m_new * scale_log2;
     l_run *= alpha;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
@@ -167,8 +175,8 @@ __global__ __launch_bounds__(256) void attn_kernel(
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float p0 = __builtin_amdgcn_exp2f(s[k2][2 * j] - m_new);
-        const float p1 = __builtin_amdgcn_exp2f(s[k2][2 * j + 1] - m_new);
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[k2][2 * j], scale_log2, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[k2][2 * j + 1], scale_log2, -mc));
         l_run += p0 + p1;
         pk[k2][j] = f2bf2(p0, p1);
       }

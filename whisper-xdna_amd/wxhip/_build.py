@@ -20,6 +20,12 @@ BUILD = ROOT / "_build"
 LIB = PKG / "libwxhip.so"
 SOURCES = ["rowops.hip", "gemm.hip", "attention.hip", "capi.cpp"]
 ARCH = "gfx950"
+# Per-file code generation options. The attention kernel feeds every MFMA
+# result straight into VALU work (softmax, rescaling); with the accumulators
+# in VGPRs (MFMA "VGPR form", supported since gfx90a) it needs no
+# v_accvgpr_read/write copies, which otherwise cost about 190 VALU slots per
+# 64-key block.
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc():
@@ -41,7 +47,8 @@ def _flags():
 
 def _compile(src):
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [hipcc(), "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)] + _flags()
+    cmd = [hipcc(), "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)] + _flags() + \
+        FILE_FLAGS.get(src, [])
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
