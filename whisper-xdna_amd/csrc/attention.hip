@@ -162,14 +162,26 @@ __global__ __launch_bounds__(256) void attn_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[k2][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-    const float mc = m_new * scale_log2;
-    l_run *= alpha;
+    // Lazy rescaling: the exponent reference m_run only moves (and O, l are
+    // rescaled by 2^((m_old - m_new) c)) when some lane's max has grown by
+    // more than 8 in the log2 domain; otherwise p = 2^(s c - m_run c) stays
+    // below 2^8, which bf16 P and the fp32 sums hold without loss. The
+    // branch is wave-uniform and, after the first block, rarely taken.
+    const bool grow = (mx - m_run) * scale_log2 > 8.0f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+      l_run *= alpha;
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+      for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run * scale_log2;
+    // P in bf16 pairs; the row sum adds exactly those bf16 values (one
+    // v_dot2_f32_bf16 per pair), the same P that multiplies V
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
     uint32_t pk[2][8];
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2)
@@ -177,10 +189,10 @@ __global__ __launch_bounds__(256) void attn_kernel(
       for (int j = 0; j < 8; ++j) {
         const float p0 = __builtin_amdgcn_exp2f(fmaf(s[k2][2 * j], scale_log2, -mc));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(s[k2][2 * j + 1], scale_log2, -mc));
-        l_run += p0 + p1;
         pk[k2][j] = f2bf2(p0, p1);
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk[k2][j]), ones,
+                                                l_run, false);
       }
-    m_run = m_new;
 
     // O^T += V^T P^T, 16 keys per MFMA; Vt rows hold each lane half's 8 keys
     // contiguously (vt_key), so one 16-byte read is the whole A fragment

@@ -62,35 +62,70 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Exact erf-GELU in fp32: 0.5*x*erfc(-x/sqrt2). The erfc form keeps full
-// relative precision in the negative tail, where 1 + erf(x/sqrt2) cancels.
+// erf-GELU, GELU(x) = x Phi(x), for every kernel that applies it (row
+// kernel and GEMM epilogues). With z = |x| / sqrt2 and t = 1 / (1 + z/2):
+//   q = x Phi(-|x|) = x (erfc(z) / 2) = x t 2^(P(t) - z^2 log2 e - 1)
+//   GELU(x) = max(x, 0) - |q|          (x - q for x >= 0, q for x < 0)
+// P is this project's own least-squares fit (weighted towards minimax) of
+// log2(erfc(z) e^(z^2) / t) on z in [0, 9.8], degree 3: |dP| < 3.9e-4, so q
+// has relative error < 2.8e-4, far below a bf16 ulp (2^-8 relative); fp32
+// evaluation over 4M inputs (the tail included) is within 1 bf16 ulp of
+// the exact GELU. The exponent is taken as 2^(arg + 32) and the 2^-33 is
+// applied by the last multiply, so results in fp32's denormal range come out
+// of an IEEE multiply instead of an exp2 that may flush them. |x| >= 16
+// returns relu(x) (|GELU - relu| < 1e-55 there), which also maps +-inf.
+// One reciprocal, one exp2 and 12 other VALU operations.
 __device__ __forceinline__ float gelu_erf(float x) {
-  return 0.5f * x * erfcf(-x * 0.70710678118654752440f);
-}
-
-// erf-GELU for GEMM epilogues, where its VALU cost competes with the MFMAs:
-// GELU(x) = x * Phi(x), Phi(-|x|) = 0.5 * erfc(|x| / sqrt2), with erfc from
-// the Chebyshev fit of Numerical Recipes (2nd ed., sec. 6.2, "erfcc":
-// erfc(z) = t * exp(-z^2 + P(t)), t = 1 / (1 + z/2), fractional error
-// < 1.2e-7 for all z >= 0). One reciprocal, one exp2 (P pre-scaled by
-// log2 e), ten FMAs. Within 1 bf16 ulp of the exact GELU for |x| < 13 (fp32
-// evaluation, relative error < 3e-5); beyond that the result is below 1e-36.
-__device__ __forceinline__ float gelu_erf_fast(float x) {
   constexpr float kL2e = 1.4426950408889634f;
   const float z = fabsf(x) * 0.70710678118654752440f;
   const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
-  float p = 0.17087277f * kL2e;
-  p = fmaf(p, t, -0.82215223f * kL2e);
-  p = fmaf(p, t, 1.48851587f * kL2e);
-  p = fmaf(p, t, -1.13520398f * kL2e);
-  p = fmaf(p, t, 0.27886807f * kL2e);
-  p = fmaf(p, t, -0.18628806f * kL2e);
-  p = fmaf(p, t, 0.09678418f * kL2e);
-  p = fmaf(p, t, 0.37409196f * kL2e);
-  p = fmaf(p, t, 1.00002368f * kL2e);
-  p = fmaf(p, t, -1.26551223f * kL2e);
-  const float e = 0.5f * t * __builtin_amdgcn_exp2f(fmaf(-z * z, kL2e, p));  // Phi(-|x|)
-  return x * (x >= 0.f ? 1.0f - e : e);
+  float p = -0.5002267360687256f;
+  p = fmaf(p, t, 0.9977306127548218f);
+  p = fmaf(p, t, 1.31719970703125f);
+  p = fmaf(p, t, -1.8143213987350464f + 32.0f);
+  const float e = __builtin_amdgcn_exp2f(fmaf(-z, z * kL2e, p));
+  const float q = (x * t) * e * 1.1641532182693481e-10f;  // 2^-33
+  const float g = fmaxf(x, 0.f) - fabsf(q);
+  return fabsf(x) < 16.0f ? g : fmaxf(x, 0.f);
+}
+
+// poly4 GELU constants: kernels/gelu_poly4_coeffs.h:4-13 (all bf16-exact;
+// the breaks {1, 2, 4} and scales {2, 2, 1} appear inline below).
+constexpr float kP4Shift[3] = {0.5f, 1.5f, 3.0f};
+constexpr float kP4Coef[3][5] = {
+    {-0.0020446777f, -0.013000488f, 0.077148438f, -0.06640625f, -0.15429688f},
+    {0.0021514893f, -0.0071716309f, -0.0040283203f, 0.063964844f, -0.10009766f},
+    {-0.0029296875f, 0.010681152f, -0.015869141f, 0.012023926f, -0.0040283203f},
+};
+
+// GELU(x) = relu(x) + q(|x|) with q the 3-piece degree-4 bump, rounded to
+// bf16 at exactly the points gelu_poly4_eval.inc rounds. x must already be
+// bf16-exact. Returns the fp32 sum before the final rounding.
+// gelu_poly4_eval.inc evaluates the pieces p = 2, 1, 0 in turn and keeps the
+// last one whose break exceeds s; that is the smallest p with s < break[p]
+// (none for s >= 4 or NaN: q = 0). Only that piece is evaluated here, with
+// its constants picked by two compares; the arithmetic on it is unchanged,
+// so the result is bit-identical.
+template <bool RNE>
+__device__ __forceinline__ float poly4_gelu_pre(float x) {
+  const float s = fabsf(x);
+  const bool in0 = s < 1.0f, in1 = s < 2.0f, in2 = s < 4.0f;
+  // piece p's constant: kP4Coef[p][k] etc., selected without indexing (an
+  // indexed constant array would be read from memory per element)
+  auto sel = [&](float c0, float c1, float c2) { return in0 ? c0 : (in1 ? c1 : c2); };
+  float t = s - sel(kP4Shift[0], kP4Shift[1], kP4Shift[2]);
+  t = RNE ? rb_rne(t) : rb_trunc(t);
+  float u = t * (in1 ? 2.0f : 1.0f);  // kP4Scale = {2, 2, 1}
+  u = RNE ? rb_rne(u) : rb_trunc(u);
+  float acc = sel(kP4Coef[0][0], kP4Coef[1][0], kP4Coef[2][0]);
+#pragma unroll
+  for (int k = 1; k <= 4; ++k) {
+    const float ah = RNE ? rb_rne(acc) : rb_trunc(acc);
+    // ah * u is exact in fp32 (two bf16 factors), so one rounding
+    acc = fmaf(ah, u, sel(kP4Coef[0][k], kP4Coef[1][k], kP4Coef[2][k]));
+  }
+  const float q = in2 ? (RNE ? rb_rne(acc) : rb_trunc(acc)) : 0.f;
+  return fmaxf(x, 0.f) + q;
 }
 
 }  // namespace wx

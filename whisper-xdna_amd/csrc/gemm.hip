@@ -24,29 +24,10 @@
 
 namespace wx {
 
-// poly4 GELU for the fc1 epilogue (g4f semantics: fp32 in, RNE). Constants
-// kernels/gelu_poly4_coeffs.h:4-13; evaluation gelu_poly4_eval.inc:27-65.
+// poly4 GELU for the fc1 epilogue (g4f semantics, kernels/gelu_row4f.cc:58-84:
+// the fp32 accumulator rounded to bf16 (RNE), then the RNE evaluation).
 __device__ __forceinline__ float epi_poly4(float xin) {
-  const float kBreak[3] = {1.0f, 2.0f, 4.0f};
-  const float kShift[3] = {0.5f, 1.5f, 3.0f};
-  const float kScale[3] = {2.0f, 2.0f, 1.0f};
-  const float kCoef[3][5] = {
-      {-0.0020446777f, -0.013000488f, 0.077148438f, -0.06640625f, -0.15429688f},
-      {0.0021514893f, -0.0071716309f, -0.0040283203f, 0.063964844f, -0.10009766f},
-      {-0.0029296875f, 0.010681152f, -0.015869141f, 0.012023926f, -0.0040283203f},
-  };
-  const float x = rb_rne(xin);
-  const float s = fabsf(x);
-  float q = 0.f;
-#pragma unroll
-  for (int p = 2; p >= 0; --p) {
-    const float u = rb_rne(rb_rne(s - kShift[p]) * kScale[p]);
-    float acc = kCoef[p][0];
-#pragma unroll
-    for (int k = 1; k <= 4; ++k) acc = fmaf(rb_rne(acc), u, kCoef[p][k]);
-    if (s < kBreak[p]) q = rb_rne(acc);
-  }
-  return fmaxf(x, 0.f) + q;
+  return poly4_gelu_pre<true>(rb_rne(xin));
 }
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
@@ -151,17 +132,17 @@ __device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&ac
           if (MODE == EPI_F32) {
             static_cast<float*>(e.out)[r0[r] + cofs[j]] = x;
           } else if (MODE == EPI_BF16) {
-            if (e.gelu == GELU_ERF) x = gelu_erf_fast(x);
+            if (e.gelu == GELU_ERF) x = gelu_erf(x);
             else if (e.gelu == GELU_POLY4_RNE) x = epi_poly4(x);
             static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(x);
           } else if (MODE == EPI_RESID) {
             float* p = static_cast<float*>(e.out) + r0[r] + cofs[j];
             *p = *p + x;
           } else if (MODE == EPI_CONV1) {
-            static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(gelu_erf_fast(x));
+            static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(gelu_erf(x));
           } else if (MODE == EPI_CONV2) {
             static_cast<float*>(e.out)[r0[r] + cofs[j]] =
-                gelu_erf_fast(x) + e.aux[(int64_t)tt[r] * N + cofs[j]];
+                gelu_erf(x) + e.aux[(int64_t)tt[r] * N + cofs[j]];
           } else {  // EPI_QKV
             const uint16_t val = f2bf(x);
             if (which[j] == 0)
@@ -232,7 +213,7 @@ __device__ __forceinline__ void store_tile_t(const EpiParams& e, const f32x16 (&
           if (MODE == EPI_CONV2) {
             const float* ap = e.aux + (int64_t)t * N + n0;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x[r] = gelu_erf_fast(x[r]) + (n0 + r < N ? ap[r] : 0.f);
+            for (int r = 0; r < 4; ++r) x[r] = gelu_erf(x[r]) + (n0 + r < N ? ap[r] : 0.f);
           }
           if (full && v32) {
             f32x4 v = {x[0], x[1], x[2], x[3]};
@@ -246,7 +227,7 @@ __device__ __forceinline__ void store_tile_t(const EpiParams& e, const f32x16 (&
         } else if (MODE == EPI_BF16 || MODE == EPI_CONV1) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (MODE == EPI_CONV1 || e.gelu == GELU_ERF) x[r] = gelu_erf_fast(x[r]);
+            if (MODE == EPI_CONV1 || e.gelu == GELU_ERF) x[r] = gelu_erf(x[r]);
             else if (e.gelu == GELU_POLY4_RNE) x[r] = epi_poly4(x[r]);
           }
           uint16_t* p = static_cast<uint16_t*>(e.out) + r0 + n0;
@@ -702,6 +683,9 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   using T128k32s6 = DCfg<128, 128, 2, 2, 32, 6>;
   using T128k64s3 = DCfg<128, 128, 2, 2, 64, 3>;
   using T256w4 = DCfg<256, 256, 2, 2, 64, 2>;
+  using T256x128s3 = DCfg<256, 128, 2, 2, 64, 3>;
+  using T256x128w8s3 = DCfg<256, 128, 4, 2, 64, 3>;
+  using T128x256w8s3 = DCfg<128, 256, 2, 4, 64, 3>;
 #define WX_TRY(NAME, CFG)                                                              \
   if (f == NAME) {                                                                     \
     if (K % CFG::BK) return hipErrorInvalidValue;                                      \
@@ -717,6 +701,9 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   WX_TRY("128x128k32s6", T128k32s6)
   WX_TRY("128x128k64s3", T128k64s3)
   WX_TRY("256x256w4", T256w4)
+  WX_TRY("256x128s3", T256x128s3)
+  WX_TRY("256x128w8s3", T256x128w8s3)
+  WX_TRY("128x256w8s3", T128x256w8s3)
 #undef WX_TRY
   // Measured on MI355X over the encoder shapes with random operands: the
   // 8-wave 256x256 tile (128x64 per wave, 2 waves per SIMD, one workgroup per

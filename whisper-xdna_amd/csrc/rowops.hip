@@ -35,6 +35,24 @@ __global__ __launch_bounds__(256) void ln_kernel(
   const int nch = cols >> 3;
   float v[MAXCH][8];
   float sum = 0.f;
+  // gamma and beta do not depend on the row: their loads are issued first so
+  // that their latency overlaps the row load and the two reductions
+  f32x4 gb[MAXCH][4];
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    const int64_t col = (int64_t)(lane + c * 64) * 8;
+    const bool ok = lane + c * 64 < nch;
+    gb[c][0] = gb[c][1] = f32x4{1.f, 1.f, 1.f, 1.f};
+    gb[c][2] = gb[c][3] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (ok && gamma) {
+      gb[c][0] = *reinterpret_cast<const f32x4*>(gamma + col);
+      gb[c][1] = *reinterpret_cast<const f32x4*>(gamma + col + 4);
+    }
+    if (ok && beta) {
+      gb[c][2] = *reinterpret_cast<const f32x4*>(beta + col);
+      gb[c][3] = *reinterpret_cast<const f32x4*>(beta + col + 4);
+    }
+  }
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) {
     const int ch = lane + c * 64;
@@ -94,15 +112,7 @@ __global__ __launch_bounds__(256) void ln_kernel(
     if (ch >= nch) continue;
     const int64_t col = (int64_t)ch * 8;
     float o[8];
-    f32x4 g0 = {1.f, 1.f, 1.f, 1.f}, g1 = g0, b0 = {0.f, 0.f, 0.f, 0.f}, b1 = b0;
-    if (gamma) {
-      g0 = *reinterpret_cast<const f32x4*>(gamma + col);
-      g1 = *reinterpret_cast<const f32x4*>(gamma + col + 4);
-    }
-    if (beta) {
-      b0 = *reinterpret_cast<const f32x4*>(beta + col);
-      b1 = *reinterpret_cast<const f32x4*>(beta + col + 4);
-    }
+    const f32x4 g0 = gb[c][0], g1 = gb[c][1], b0 = gb[c][2], b1 = gb[c][3];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       o[j] = (v[c][j] - mean) * rstd * g0[j] + b0[j];
@@ -163,41 +173,6 @@ hipError_t launch_layernorm(const void* x, int x_dtype, int64_t ldx,
 }
 
 // ======================================================== GELU
-// poly4 constants: kernels/gelu_poly4_coeffs.h:4-13 (all bf16-exact).
-__constant__ float kP4Break[3] = {1.0f, 2.0f, 4.0f};
-__constant__ float kP4Shift[3] = {0.5f, 1.5f, 3.0f};
-__constant__ float kP4Scale[3] = {2.0f, 2.0f, 1.0f};
-__constant__ float kP4Coef[3][5] = {
-    {-0.0020446777f, -0.013000488f, 0.077148438f, -0.06640625f, -0.15429688f},
-    {0.0021514893f, -0.0071716309f, -0.0040283203f, 0.063964844f, -0.10009766f},
-    {-0.0029296875f, 0.010681152f, -0.015869141f, 0.012023926f, -0.0040283203f},
-};
-
-// GELU(x) = relu(x) + q(|x|) with q the 3-piece degree-4 bump, rounded to
-// bf16 at exactly the points gelu_poly4_eval.inc rounds. x must already be
-// bf16-exact. Returns the fp32 sum before the final rounding.
-template <bool RNE>
-__device__ __forceinline__ float poly4_gelu_pre(float x) {
-  const float s = fabsf(x);
-  float q = 0.f;
-#pragma unroll
-  for (int p = 2; p >= 0; --p) {
-    float t = s - kP4Shift[p];
-    t = RNE ? rb_rne(t) : rb_trunc(t);
-    float u = t * kP4Scale[p];
-    u = RNE ? rb_rne(u) : rb_trunc(u);
-    float acc = kP4Coef[p][0];
-#pragma unroll
-    for (int k = 1; k <= 4; ++k) {
-      const float ah = RNE ? rb_rne(acc) : rb_trunc(acc);
-      // ah * u is exact in fp32 (two bf16 factors), so one rounding
-      acc = fmaf(ah, u, kP4Coef[p][k]);
-    }
-    if (s < kP4Break[p]) q = RNE ? rb_rne(acc) : rb_trunc(acc);
-  }
-  return fmaxf(x, 0.f) + q;
-}
-
 __device__ __forceinline__ uint16_t gelu_variant(float x, int variant) {
   if (variant == GELU_ERF) return f2bf(gelu_erf(x));
   if (variant == GELU_POLY4_RNE) return f2bf(poly4_gelu_pre<true>(rb_rne(x)));
@@ -364,6 +339,102 @@ __global__ __launch_bounds__(256) void softmax_kernel(
   }
 }
 
+// Rows whose start is not 16-byte aligned (a row pitch that is not a
+// multiple of 8 elements, e.g. 1500): the row is read as the 16-byte chunks of
+// the aligned span that covers it, chunk c holding elements 8 c - head ..
+// 8 c - head + 7 of the row (head = row start mod 8). Only the first and last
+// chunk can hold elements outside the row; those are masked to -inf for the
+// max and written element by element, every other chunk is one 16-byte load
+// and one 16-byte store. Loads go through a buffer descriptor that covers
+// exactly the input; the last row's last chunk, the only one that can reach
+// past the input's end, is read element by element.
+// exp is one FMA and one exp2 per element: p = 2^(x log2e - m log2e + 32)
+// / sum; the +32 keeps exp2's result out of the denormal range for every p
+// that is representable, and cancels in the division.
+template <int MAXCH>
+__global__ __launch_bounds__(256) void softmax_kernel_span(
+    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y,
+    int64_t ldy, int rows, int valid, int x_bytes) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, x_bytes, 0x00020000);
+  const int64_t sx = (int64_t)row * ldx, sy = (int64_t)row * ldy;
+  const int head = (int)(sx & 7);
+  const int64_t ax = sx - head, ay = sy - head;  // ldx == ldy (mod 8): same head
+  const int nch = (head + valid + 7) >> 3;
+  float v[MAXCH][8];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) {
+    const int c = lane + i * 64;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[i][j] = -INFINITY;
+    if (c < nch) {
+      if (row == rows - 1 && c == nch - 1) {
+        // the one chunk that may run past the end of the input: a 16-byte
+        // access that crosses the descriptor's range reads as all zeros, so
+        // its in-row elements are read one by one
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int e = c * 8 + j - head;
+          if (e >= 0 && e < valid) v[i][j] = bf2f(x[sx + e]);
+        }
+      } else {
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)((ax + c * 8) * 2), 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[i][2 * j] = __uint_as_float(w[j] << 16);
+          v[i][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+        }
+      }
+      if (c == 0 || c == nch - 1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int e = c * 8 + j - head;
+          if (e < 0 || e >= valid) v[i][j] = -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, v[i][j]);
+    }
+  }
+  m = wave_max(m);
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float off = 32.0f - m * kLog2e;
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) {
+    if (lane + i * 64 < nch) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[i][j] = __builtin_amdgcn_exp2f(fmaf(v[i][j], kLog2e, off));
+        sum += v[i][j];
+      }
+    }
+  }
+  const float inv = 1.0f / wave_sum(sum);
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) {
+    const int c = lane + i * 64;
+    if (c >= nch) continue;
+    if (c == 0 || c == nch - 1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = c * 8 + j - head;
+        if (e >= 0 && e < valid) y[ay + c * 8 + j] = f2bf(v[i][j] * inv);
+      }
+    } else {
+      u32x4 pk;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pk[j] = f2bf2(v[i][2 * j] * inv, v[i][2 * j + 1] * inv);
+      *reinterpret_cast<u32x4*>(y + ay + c * 8) = pk;
+    }
+  }
+#endif
+}
+
 // Rows wider than the register budget: three passes over global memory.
 __global__ __launch_bounds__(256) void softmax_kernel_wide(
     const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y,
@@ -392,8 +463,15 @@ hipError_t launch_softmax(const uint16_t* x, int64_t ldx, uint16_t* y,
     return valid % vec == 0 && ldx % vec == 0 && ldy % vec == 0 &&
            (uintptr_t)x % (vec * 2) == 0 && (uintptr_t)y % (vec * 2) == 0;
   };
+  const int64_t x_bytes = ((int64_t)(rows - 1) * ldx + valid) * 2;
+  const bool span = ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 &&
+                    (ldx - ldy) % 8 == 0 && x_bytes < (1ll << 31);
   if (valid <= 64 * 8 * 8 && aligned(8))
     softmax_kernel<8, 8><<<grid, block, 0, s>>>(x, ldx, y, ldy, rows, valid);
+  else if (span && valid + 7 <= 64 * 8 * 4)
+    softmax_kernel_span<4><<<grid, block, 0, s>>>(x, ldx, y, ldy, rows, valid, (int)x_bytes);
+  else if (span && valid + 7 <= 64 * 8 * 8)
+    softmax_kernel_span<8><<<grid, block, 0, s>>>(x, ldx, y, ldy, rows, valid, (int)x_bytes);
   else if (valid <= 64 * 4 * 16 && aligned(4))
     softmax_kernel<4, 16><<<grid, block, 0, s>>>(x, ldx, y, ldy, rows, valid);
   else if (valid <= 64 * 32)

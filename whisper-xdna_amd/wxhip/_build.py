@@ -21,11 +21,13 @@ LIB = PKG / "libwxhip.so"
 SOURCES = ["rowops.hip", "gemm.hip", "attention.hip", "capi.cpp"]
 ARCH = "gfx950"
 # Per-file code generation options. The attention kernel feeds every MFMA
-# result straight into VALU work (softmax, rescaling); with the accumulators
-# in VGPRs (MFMA "VGPR form", supported since gfx90a) it needs no
-# v_accvgpr_read/write copies, which otherwise cost about 190 VALU slots per
-# 64-key block.
-FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# result straight into VALU work (softmax, rescaling), and the GEMM
+# epilogues read every accumulator once; with the accumulators in VGPRs
+# (MFMA "VGPR form", supported since gfx90a) neither needs
+# v_accvgpr_read/write copies (about 190 VALU slots per 64-key attention
+# block).
+_VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+FILE_FLAGS = {"attention.hip": _VGPR_MFMA, "gemm.hip": _VGPR_MFMA}
 
 
 def hipcc():
