@@ -30,6 +30,15 @@ sys.path[:0] = [str(ROOT / "whisper-xdna_amd"), str(ROOT)]
 METRIC = "large-v3 encoder ms @ctx=1500 bs=1; mel-frames/s bs=16; % bf16 MFMA peak"
 PEAK_BF16 = 2.5e15      # MI355X dense bf16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12       # MI355X HBM3E, B/s
+# HBM-side bytes per launch of the kernels that can be the dominant stage,
+# measured with `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over
+# whisper-xdna_amd/wxhip/probe.py at the batch-16 shape, each counter scaled
+# by what it reads for a 512 MiB device copy (FETCH_SIZE x 2.000, WRITE_SIZE
+# x 1.000); the summaries, with their commands, are in profiles/.
+TRAFFIC_BYTES = {
+    "fc1": (1.0024e9, "profiles/gemm_fc1_l16_traffic.md"),
+    "attention": (1.146e9, "profiles/attention_l16_traffic.md"),
+}
 LARGE = dict(n_mels=128, d=1280, n_head=20, n_layer=32, n_ctx=1500)
 WORKLOADS = {
     "l16": dict(batch=16, n_frames=3000,
@@ -90,13 +99,16 @@ def rowop_bandwidth(dev):
     out = {}
     specs = [
         ("layernorm_1500x1280_bf16", (1500, 1280), 80),
+        # the encoder's own LayerNorm: fp32 residual in, bf16 out, batch 16
+        ("layernorm_24000x1280_f32_to_bf16", (24000, 1280), 4),
         ("gelu_erf_1500x5120_bf16", (1500, 5120), 24),
         ("gelu_poly4_1500x5120_bf16", (1500, 5120), 24),
         ("softmax_30000x1500_bf16", (30000, 1500), 4),
     ]
     for name, shape, nset in specs:
-        xs = [torch.randn(shape, device=dev.device).to(torch.bfloat16) for _ in range(nset)]
-        ys = [torch.empty_like(xs[0]) for _ in range(nset)]
+        xdt = torch.float32 if "f32_to" in name else torch.bfloat16
+        xs = [torch.randn(shape, device=dev.device).to(xdt) for _ in range(nset)]
+        ys = [torch.empty(shape, dtype=torch.bfloat16, device=dev.device) for _ in range(nset)]
         g = torch.ones(shape[1], device=dev.device)
         b = torch.zeros(shape[1], device=dev.device)
 
@@ -127,7 +139,7 @@ def rowop_bandwidth(dev):
         e1.record()
         torch.cuda.synchronize()
         per = e0.elapsed_time(e1) / 1e3 / (reps * nset)
-        nbytes = 2 * 2 * shape[0] * shape[1]
+        nbytes = (xs[0].element_size() + 2) * shape[0] * shape[1]
         gbs = nbytes / per / 1e9
         out[name] = {"us": round(per * 1e6, 2), "GB/s": round(gbs, 1),
                      "hbm_frac": round(gbs * 1e9 / PEAK_HBM, 3),
@@ -235,7 +247,9 @@ def main():
         "encoder_mfma_frac": round(total_flops / dt / PEAK_BF16, 4),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                     "frac": round(achieved * 1e12 / PEAK_BF16, 4),
+                     "traffic": TRAFFIC_BYTES[dom][0] if dom in TRAFFIC_BYTES else None,
+                     "traffic_source": TRAFFIC_BYTES[dom][1] if dom in TRAFFIC_BYTES else None,
                      "flop_per_launch": flop_per_launch,
                      "avg_launch_us": round(per_launch_s * 1e6, 2)},
         "stages": kern,

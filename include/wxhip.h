@@ -79,7 +79,10 @@ const char* wxh_last_error(void);
  * context/overlay bookkeeping). No per-shape compile, no context ceiling. */
 int wxh_create(int device, wxh_ctx** out);
 
-/* Destroy a context (synchronises its stream first). */
+/* Release the caller's hold on a context. Encoders created on it keep it
+ * alive; the context (its stream synchronised first) is freed when the last
+ * of the caller and those encoders lets go, so wxh_destroy and
+ * wxh_encoder_destroy may come in either order. */
 int wxh_destroy(wxh_ctx* ctx);
 
 /* Set the fault-injection mask (0 = off). */
@@ -190,6 +193,7 @@ typedef struct {
  * uploaded once, nothing is evicted. */
 int wxh_encoder_create(wxh_ctx* ctx, const wxh_encoder_dims* dims,
                        wxh_encoder** out);
+/* Free an encoder (and its hold on its context). */
 int wxh_encoder_destroy(wxh_encoder* enc);
 
 /* Upload one weight from host fp32 by its whisper state-dict name, with or

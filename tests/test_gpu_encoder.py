@@ -176,3 +176,19 @@ def test_fallback_on_injected_c_abi_failure(dev, tiny):
     assert not rt.graph_ok and len(rt.fallbacks) == 1
     assert cosine(out, OE.encoder_torch(tiny, mel)) >= 0.9999
     rt.dev.set_fail_inject(0)
+
+
+def test_context_released_before_encoder(tiny):
+    """wxh_destroy of a context before wxh_encoder_destroy of an encoder made
+    on it (an order Python's cycle collector may pick) must leave the encoder
+    usable and free the context only with its last holder."""
+    import wxhip
+    case("context released before its encoder")
+    own = wxhip.Device(0)
+    enc = wxhip.HipEncoder(own, tiny, n_layer=1)
+    mel = synth.make_mel(80, 200, seed=5)
+    before = _fwd(enc, mel, own)
+    own.close()                      # wxh_destroy: the encoder still holds the context
+    after = _fwd(enc, mel, own)
+    np.testing.assert_array_equal(before, after)
+    enc.close()                      # last holder: the context is freed here

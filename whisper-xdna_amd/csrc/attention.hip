@@ -59,9 +59,15 @@ __global__ __launch_bounds__(256) void attn_kernel(
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int w = tid >> 6;
-  const int h = blockIdx.y, b = blockIdx.z;
+  // the query blocks of one head run on one XCD, which then fetches that
+  // head's K and Vt into its L2 once instead of once per XCD
+  const int nqb = gridDim.x;
+  const int pid = xcd_remap(blockIdx.x + nqb * (blockIdx.y + gridDim.y * blockIdx.z),
+                            nqb * gridDim.y * gridDim.z);
+  const int qb = pid % nqb;
+  const int h = (pid / nqb) % n_head, b = pid / (nqb * n_head);
   const int64_t bh = (int64_t)b * n_head + h;
-  const int q0 = blockIdx.x * kQB + w * 32;
+  const int q0 = qb * kQB + w * 32;
   const uint16_t* Qh = Q + bh * Tp * kHeadDim;
   const uint16_t* Kh = K + bh * Tp * kHeadDim;
   const uint16_t* Vh = Vt + bh * kHeadDim * Tp;

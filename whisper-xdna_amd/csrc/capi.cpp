@@ -14,6 +14,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <string>
@@ -54,10 +55,15 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+// A context is shared by its caller and by every encoder created on it; it
+// is freed when the last of them lets go (wxh_destroy and
+// wxh_encoder_destroy each drop one reference), so an encoder may be
+// destroyed after wxh_destroy of its context, in either order.
 struct wxh_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   uint32_t fail_mask = 0;
+  std::atomic<int> refs{1};
 };
 
 namespace {
@@ -107,12 +113,19 @@ int wxh_create(int device, wxh_ctx** out) {
   return WXH_OK;
 }
 
-int wxh_destroy(wxh_ctx* c) {
-  if (!c) return WXH_OK;
+namespace {
+void ctx_release(wxh_ctx* c) {
+  if (c->refs.fetch_sub(1) != 1) return;
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   (void)hipStreamDestroy(c->stream);
   delete c;
+}
+}  // namespace
+
+int wxh_destroy(wxh_ctx* c) {
+  if (!c) return WXH_OK;
+  ctx_release(c);
   return WXH_OK;
 }
 
@@ -671,6 +684,7 @@ int wxh_encoder_create(wxh_ctx* c, const wxh_encoder_dims* dims, wxh_encoder** o
     delete E;
     return r;
   }
+  c->refs.fetch_add(1);
   *out = E;
   return WXH_OK;
 }
@@ -683,7 +697,9 @@ int wxh_encoder_destroy(wxh_encoder* E) {
   free_list(E->ws_allocs);
   free_list(E->allocs);
   if (E->stage) (void)hipFree(E->stage);
+  wxh_ctx* c = E->ctx;
   delete E;
+  ctx_release(c);
   return WXH_OK;
 }
 

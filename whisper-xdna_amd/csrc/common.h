@@ -62,6 +62,23 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each
+// XCD has its own L2. xcd_remap(id, total) renumbers ids so that the ids one
+// XCD receives (id % 8 == x) are one contiguous run of [0, total): work
+// items that are numbered next to each other (tiles sharing operands, query
+// blocks of one head) then share an L2.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int xcd_remap(int pid, int total) {
+  const int per = (total + kXcds - 1) / kXcds;
+  int tall = total % kXcds;
+  if (tall == 0) tall = kXcds;
+  const int xcd = pid % kXcds, local = pid / kXcds;
+  return xcd < tall ? xcd * per + local
+                    : tall * per + (xcd - tall) * (per - 1) + local;
+}
+
+
 // erf-GELU, GELU(x) = x Phi(x), for every kernel that applies it (row
 // kernel and GEMM epilogues). With z = |x| / sqrt2 and t = 1 / (1 + z/2):
 //   q = x Phi(-|x|) = x (erfc(z) / 2) = x t 2^(P(t) - z^2 log2 e - 1)

@@ -443,17 +443,7 @@ struct DCfg {
 // W columns in L2 / the Infinity Cache. xcd_remap renumbers tile ids so that
 // the ids one XCD receives (every 8th, round-robin dispatch) are a
 // contiguous run of that order.
-constexpr int kXcds = 8;
 constexpr int kGroupM = 16;
-
-__device__ __forceinline__ int xcd_remap(int pid, int total) {
-  const int per = (total + kXcds - 1) / kXcds;
-  int tall = total % kXcds;
-  if (tall == 0) tall = kXcds;
-  const int xcd = pid % kXcds, local = pid / kXcds;
-  return xcd < tall ? xcd * per + local
-                    : tall * per + (xcd - tall) * (per - 1) + local;
-}
 
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4],
 // lgkmcnt[11:8]; the other two counters left at their maximum, i.e. not
