@@ -664,36 +664,20 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   const std::string f = force ? force : "";
   if (!dma || f == "v1") return gemm_launch_cfg<Cfg128>(M, N, K, a, W, ldw, mode, e, s);
   using T128 = DCfg<128, 128, 2, 2, 64, 2>;
-  using T128k32s4 = DCfg<128, 128, 2, 2, 32, 4>;
   using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
+  // deeper rings (BK 32, 4 slots), kept for comparison: on MI355X they move
+  // the same bytes in the same time as the 2-slot BK 64 ring
+  using T128k32s4 = DCfg<128, 128, 2, 2, 32, 4>;
   using T256w8k32s4 = DCfg<256, 256, 2, 4, 32, 4>;
-  using T256x128w8k32s4 = DCfg<256, 128, 4, 2, 32, 4>;
-  using T256x128k64s2 = DCfg<256, 128, 2, 2, 64, 2>;
-  using T256w8k32s5 = DCfg<256, 256, 2, 4, 32, 5>;
-  using T128k32s6 = DCfg<128, 128, 2, 2, 32, 6>;
-  using T128k64s3 = DCfg<128, 128, 2, 2, 64, 3>;
-  using T256w4 = DCfg<256, 256, 2, 2, 64, 2>;
-  using T256x128s3 = DCfg<256, 128, 2, 2, 64, 3>;
-  using T256x128w8s3 = DCfg<256, 128, 4, 2, 64, 3>;
-  using T128x256w8s3 = DCfg<128, 256, 2, 4, 64, 3>;
 #define WX_TRY(NAME, CFG)                                                              \
   if (f == NAME) {                                                                     \
     if (K % CFG::BK) return hipErrorInvalidValue;                                      \
     return gemm_dma_launch<CFG>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);     \
   }
   WX_TRY("128x128", T128)
-  WX_TRY("128x128k32s4", T128k32s4)
   WX_TRY("256x256w8", T256w8)
+  WX_TRY("128x128k32s4", T128k32s4)
   WX_TRY("256x256w8k32s4", T256w8k32s4)
-  WX_TRY("256x128w8k32s4", T256x128w8k32s4)
-  WX_TRY("256x128", T256x128k64s2)
-  WX_TRY("256x256w8k32s5", T256w8k32s5)
-  WX_TRY("128x128k32s6", T128k32s6)
-  WX_TRY("128x128k64s3", T128k64s3)
-  WX_TRY("256x256w4", T256w4)
-  WX_TRY("256x128s3", T256x128s3)
-  WX_TRY("256x128w8s3", T256x128w8s3)
-  WX_TRY("128x256w8s3", T128x256w8s3)
 #undef WX_TRY
   // Measured on MI355X over the encoder shapes with random operands: the
   // 8-wave 256x256 tile (128x64 per wave, 2 waves per SIMD, one workgroup per
