@@ -164,56 +164,72 @@ __device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&ac
 // g < 4. Each lane then writes four runs of 4 consecutive columns: 8-byte
 // (bf16) or 16-byte (fp32) stores and loads, one row's address math per
 // block row, and a read-modify-write of the fp32 residual in 16-byte pieces.
-// Column runs that cross N, or outputs whose row stride or base are not
-// aligned for the vector access, take the scalar path.
-template <int MODE, int TM, int TN>
-__device__ __forceinline__ void store_tile_t(const EpiParams& e, const f32x16 (&acc)[TM][TN],
-                                             int M, int N, int row0, int col0, int lane) {
-  const int l32 = lane & 31, half = lane >> 5;
-  const uintptr_t ob = (uintptr_t)e.out;
-  const bool v32 = (e.ldo & 3) == 0 && (ob & 15) == 0;  // fp32 runs are 16-byte aligned
-  const bool v16 = (e.ldo & 3) == 0 && (ob & 7) == 0;   // bf16 runs are 8-byte aligned
-  const bool vb = ((uintptr_t)e.bias & 15) == 0;
-  f32x4 bias[TN][4];
+//
+// The bias of those columns is loaded before the main loop (load_bias), so
+// its latency is long gone when the epilogue runs. The activation is part of
+// MODE, so each kernel carries one epilogue only. A wave tile that lies
+// wholly inside C with aligned outputs (every tile but the edge ones) takes
+// the unchecked path; the others check every row, column run and alignment.
+template <int TN>
+__device__ __forceinline__ void load_bias(const float* bias, int N, int col0, int lane,
+                                          f32x4 (&bv)[TN][4]) {
+  const int half = lane >> 5;
+  const bool vb = ((uintptr_t)bias & 15) == 0;
   static_for<TN>([&](auto j) {
     static_for<4>([&](auto g) {
       const int n0 = col0 + j * 32 + g * 8 + half * 4;
-      if (e.bias && vb && n0 + 3 < N) {
-        bias[j][g] = *reinterpret_cast<const f32x4*>(e.bias + n0);
+      if (bias && vb && n0 + 3 < N) {
+        bv[j][g] = *reinterpret_cast<const f32x4*>(bias + n0);
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) bias[j][g][r] = (e.bias && n0 + r < N) ? e.bias[n0 + r] : 0.f;
+        for (int r = 0; r < 4; ++r) bv[j][g][r] = (bias && n0 + r < N) ? bias[n0 + r] : 0.f;
       }
     });
   });
+}
+
+template <int MODE, int TM, int TN, bool CHECKED>
+__device__ __forceinline__ void store_tile_t_impl(const EpiParams& e, const f32x16 (&acc)[TM][TN],
+                                                  const f32x4 (&bv)[TN][4], int M, int N,
+                                                  int row0, int col0, int lane) {
+  const int l32 = lane & 31, half = lane >> 5;
+  const uintptr_t ob = (uintptr_t)e.out;
+  const bool v32 = !CHECKED || ((e.ldo & 3) == 0 && (ob & 15) == 0);  // fp32 runs 16-byte aligned
+  const bool v16 = !CHECKED || ((e.ldo & 3) == 0 && (ob & 7) == 0);   // bf16 runs 8-byte aligned
   static_for<TM>([&](auto i) {
     const int m = row0 + i * 32 + l32;
-    if (m >= M) return;
-    const int T = e.rows_per_batch;
-    const int b = m / T, t = m - b * T;
+    if (CHECKED && m >= M) return;
+    int t = m;
     int64_t r0, r1 = 0;
-    if (MODE == EPI_CONV1) {
-      r0 = (int64_t)b * e.out_batch_stride + (int64_t)(t + 1) * e.ldo;
-    } else if (MODE == EPI_QKV) {
-      r0 = ((int64_t)b * e.n_head * e.t_pad + t) * 64;
-      r1 = (int64_t)b * e.n_head * 64 * e.t_pad + vt_key(t);
+    if (MODE == EPI_CONV1 || MODE == EPI_CONV2 || MODE == EPI_QKV) {
+      const int T = e.rows_per_batch;
+      const int b = m / T;
+      t = m - b * T;
+      if (MODE == EPI_CONV1) {
+        r0 = (int64_t)b * e.out_batch_stride + (int64_t)(t + 1) * e.ldo;
+      } else if (MODE == EPI_QKV) {
+        r0 = ((int64_t)b * e.n_head * e.t_pad + t) * 64;
+        r1 = (int64_t)b * e.n_head * 64 * e.t_pad + vt_key(t);
+      } else {
+        r0 = (int64_t)m * e.ldo;
+      }
     } else {
       r0 = (int64_t)m * e.ldo;
     }
     static_for<TN>([&](auto j) {
       static_for<4>([&](auto g) {
         const int n0 = col0 + j * 32 + g * 8 + half * 4;
-        if (n0 >= N) return;
-        const bool full = n0 + 3 < N;
+        if (CHECKED && n0 >= N) return;
+        const bool full = !CHECKED || n0 + 3 < N;
         float x[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = acc[i][j][g * 4 + r] + bias[j][g][r];
+        for (int r = 0; r < 4; ++r) x[r] = acc[i][j][g * 4 + r] + bv[j][g][r];
         if (MODE == EPI_F32 || MODE == EPI_RESID || MODE == EPI_CONV2) {
           float* p = static_cast<float*>(e.out) + r0 + n0;
           if (MODE == EPI_CONV2) {
             const float* ap = e.aux + (int64_t)t * N + n0;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x[r] = gelu_erf(x[r]) + (n0 + r < N ? ap[r] : 0.f);
+            for (int r = 0; r < 4; ++r) x[r] = gelu_erf(x[r]) + (full || n0 + r < N ? ap[r] : 0.f);
           }
           if (full && v32) {
             f32x4 v = {x[0], x[1], x[2], x[3]};
@@ -224,11 +240,12 @@ __device__ __forceinline__ void store_tile_t(const EpiParams& e, const f32x16 (&
             for (int r = 0; r < 4; ++r)
               if (n0 + r < N) p[r] = MODE == EPI_RESID ? p[r] + x[r] : x[r];
           }
-        } else if (MODE == EPI_BF16 || MODE == EPI_CONV1) {
+        } else if (MODE == EPI_BF16 || MODE == EPI_BF16_GELU || MODE == EPI_BF16_POLY4 ||
+                   MODE == EPI_CONV1) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (MODE == EPI_CONV1 || e.gelu == GELU_ERF) x[r] = gelu_erf(x[r]);
-            else if (e.gelu == GELU_POLY4_RNE) x[r] = epi_poly4(x[r]);
+            if (MODE == EPI_CONV1 || MODE == EPI_BF16_GELU) x[r] = gelu_erf(x[r]);
+            if (MODE == EPI_BF16_POLY4) x[r] = epi_poly4(x[r]);
           }
           uint16_t* p = static_cast<uint16_t*>(e.out) + r0 + n0;
           if (full && v16) {
@@ -256,6 +273,21 @@ __device__ __forceinline__ void store_tile_t(const EpiParams& e, const f32x16 (&
       });
     });
   });
+}
+
+template <int MODE, int TM, int TN>
+__device__ __forceinline__ void store_tile_t(const EpiParams& e, const f32x16 (&acc)[TM][TN],
+                                             const f32x4 (&bv)[TN][4], int M, int N, int row0,
+                                             int col0, int lane) {
+  const uintptr_t ob = (uintptr_t)e.out;
+  const bool aligned = (e.ldo & 3) == 0 && (ob & 15) == 0;
+  const bool interior = row0 + TM * 32 <= M && col0 + TN * 32 <= N &&
+                        (MODE == EPI_QKV || MODE == EPI_CONV1 || aligned) &&
+                        (MODE != EPI_CONV2 || (N & 3) == 0);
+  if (interior)
+    store_tile_t_impl<MODE, TM, TN, false>(e, acc, bv, M, N, row0, col0, lane);
+  else
+    store_tile_t_impl<MODE, TM, TN, true>(e, acc, bv, M, N, row0, col0, lane);
 }
 
 template <class C, int MODE>
@@ -527,6 +559,9 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     for (int j = 0; j < C::TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  // issued ahead of the DMA prologue, so the first stage wait covers it too
+  f32x4 bv[C::TN][4];
+  load_bias<C::TN>(e.bias, N, bn0 + wn * C::WTN, lane, bv);
 
   const int nk = K / C::BK;
   const int sw = (l32 / C::RPW) % C::CPR;  // the swizzle of every row this lane reads
@@ -593,7 +628,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  store_tile_t<MODE, C::TM, C::TN>(e, acc, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
+  store_tile_t<MODE, C::TM, C::TN>(e, acc, bv, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
 #endif
 }
 
@@ -625,9 +660,11 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const uin
     gemm_dma_kernel<C, MD><<<grid, block, 0, s>>>(M, N, K, a, W, ldw, e, a_bytes,   \
                                                   w_bytes, group_m, remap);          \
     break;
+  if (mode == EPI_BF16 && e.gelu == GELU_ERF) mode = EPI_BF16_GELU;
+  if (mode == EPI_BF16 && e.gelu == GELU_POLY4_RNE) mode = EPI_BF16_POLY4;
   switch (mode) {
     WX_DMA(EPI_F32) WX_DMA(EPI_BF16) WX_DMA(EPI_RESID) WX_DMA(EPI_CONV1)
-    WX_DMA(EPI_CONV2) WX_DMA(EPI_QKV)
+    WX_DMA(EPI_CONV2) WX_DMA(EPI_QKV) WX_DMA(EPI_BF16_GELU) WX_DMA(EPI_BF16_POLY4)
     default:
       return hipErrorInvalidValue;
   }
@@ -681,13 +718,11 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
 #undef WX_TRY
   // Measured on MI355X over the encoder shapes with random operands: the
   // 8-wave 256x256 tile (128x64 per wave, 2 waves per SIMD, one workgroup per
-  // CU) is fastest for the narrow outputs (N <= 2048: out-proj, fc2) once
-  // there are enough tiles to fill the 256 CUs. For wide outputs (fc1, QKV)
-  // the 128x128 tile wins: two workgroups share a CU, so one's epilogue (the
-  // GELU and the bf16 stores of a large output) overlaps the other's main
-  // loop. At batch 1 the 128x128 tile also keeps more CUs busy.
+  // CU) is fastest once there are enough tiles to fill the 256 CUs (batch 16:
+  // fc1 367 us vs 399 for 128x128, QKV 269 vs 295, fc2 319 vs 370). Below
+  // that (batch 1) the 128x128 tile keeps more CUs busy.
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-  if (big_tiles >= 256 && N <= 2048)
+  if (big_tiles >= 256)
     return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
 }

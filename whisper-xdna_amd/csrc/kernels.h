@@ -50,6 +50,10 @@ enum EpiMode {
   EPI_CONV1 = 3,   // padded bf16 out row (t + 1) of batch b = gelu_erf(acc + bias)
   EPI_CONV2 = 4,   // resid fp32 = gelu_erf(acc + bias) + aux[t, n]
   EPI_QKV = 5,     // split into head-major Q, K and transposed V (bf16)
+  // EPI_BF16 with the activation fixed at compile time (chosen by launch_gemm
+  // from EpiParams::gelu; callers pass EPI_BF16)
+  EPI_BF16_GELU = 6,   // out bf16 = gelu_erf(acc + bias)
+  EPI_BF16_POLY4 = 7,  // out bf16 = poly4 GELU (g4f) of acc + bias
 };
 
 struct GemmA {
