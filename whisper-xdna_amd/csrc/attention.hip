@@ -58,7 +58,9 @@ __global__ __launch_bounds__(256) void attn_kernel(
   const int lane = tid & 63;
   const int half = lane >> 5;
   const int l32 = lane & 31;
-  const int w = tid >> 6;
+  // wave index: uniform across the wave; readfirstlane makes that visible
+  // to the compiler, so everything derived from it stays in SGPRs
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // the query blocks of one head run on one XCD, which then fetches that
   // head's K and Vt into its L2 once instead of once per XCD
   const int nqb = gridDim.x;

@@ -174,18 +174,27 @@ template <int TN>
 __device__ __forceinline__ void load_bias(const float* bias, int N, int col0, int lane,
                                           f32x4 (&bv)[TN][4]) {
   const int half = lane >> 5;
-  const bool vb = ((uintptr_t)bias & 15) == 0;
-  static_for<TN>([&](auto j) {
-    static_for<4>([&](auto g) {
-      const int n0 = col0 + j * 32 + g * 8 + half * 4;
-      if (bias && vb && n0 + 3 < N) {
-        bv[j][g] = *reinterpret_cast<const f32x4*>(bias + n0);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bv[j][g][r] = (bias && n0 + r < N) ? bias[n0 + r] : 0.f;
-      }
+  // uniform branches only: a guarded element-wise path would make the
+  // compiler wait for each load in turn, before the DMA prologue is issued
+  if (bias == nullptr) {
+    static_for<TN>([&](auto j) {
+      static_for<4>([&](auto g) { bv[j][g] = f32x4{0.f, 0.f, 0.f, 0.f}; });
     });
-  });
+  } else if (((uintptr_t)bias & 15) == 0 && col0 + TN * 32 <= N) {
+    static_for<TN>([&](auto j) {
+      static_for<4>([&](auto g) {
+        bv[j][g] = *reinterpret_cast<const f32x4*>(bias + col0 + j * 32 + g * 8 + half * 4);
+      });
+    });
+  } else {
+    static_for<TN>([&](auto j) {
+      static_for<4>([&](auto g) {
+        const int n0 = col0 + j * 32 + g * 8 + half * 4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bv[j][g][r] = n0 + r < N ? bias[n0 + r] : 0.f;
+      });
+    });
+  }
 }
 
 template <int MODE, int TM, int TN, bool CHECKED>
@@ -216,6 +225,21 @@ __device__ __forceinline__ void store_tile_t_impl(const EpiParams& e, const f32x
     } else {
       r0 = (int64_t)m * e.ldo;
     }
+    // The residual (EPI_RESID) or positional embedding (EPI_CONV2) of this
+    // block row is read in one batch before any of its stores: issued after
+    // a store, each load would wait out a full memory round trip on its own
+    // (the compiler cannot move loads above stores that may alias).
+    f32x4 pre[TN][4];
+    if (!CHECKED && (MODE == EPI_RESID || MODE == EPI_CONV2)) {
+      static_for<TN>([&](auto j) {
+        static_for<4>([&](auto g) {
+          const int n0 = col0 + j * 32 + g * 8 + half * 4;
+          pre[j][g] = MODE == EPI_RESID
+                          ? *reinterpret_cast<const f32x4*>(static_cast<const float*>(e.out) + r0 + n0)
+                          : *reinterpret_cast<const f32x4*>(e.aux + (int64_t)t * N + n0);
+        });
+      });
+    }
     static_for<TN>([&](auto j) {
       static_for<4>([&](auto g) {
         const int n0 = col0 + j * 32 + g * 8 + half * 4;
@@ -226,6 +250,16 @@ __device__ __forceinline__ void store_tile_t_impl(const EpiParams& e, const f32x
         for (int r = 0; r < 4; ++r) x[r] = acc[i][j][g * 4 + r] + bv[j][g][r];
         if (MODE == EPI_F32 || MODE == EPI_RESID || MODE == EPI_CONV2) {
           float* p = static_cast<float*>(e.out) + r0 + n0;
+          if (!CHECKED) {
+            f32x4 v = {x[0], x[1], x[2], x[3]};
+            if (MODE == EPI_CONV2) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) v[r] = gelu_erf(v[r]) + pre[j][g][r];
+            }
+            if (MODE == EPI_RESID) v += pre[j][g];
+            *reinterpret_cast<f32x4*>(p) = v;
+            return;
+          }
           if (MODE == EPI_CONV2) {
             const float* ap = e.aux + (int64_t)t * N + n0;
 #pragma unroll
@@ -501,7 +535,9 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  // wave index: uniform across the wave; readfirstlane makes that visible
+  // to the compiler, so everything derived from it stays in SGPRs
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w / C::WN, wn = w % C::WN;
   const int l32 = lane & 31, half = lane >> 5;
 
