@@ -23,6 +23,8 @@
 // and the correction factor is one scalar per lane. P^T is repacked to bf16
 // in registers and multiplied as O^T += V^T P^T; V^T's k-slots are read from
 // LDS in exactly the key order the score fragment left in each lane.
+#include <utility>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -46,6 +48,16 @@ __device__ __forceinline__ void wait_vm() {
 // instruction, lane l at byte 16 l). Rows are 128 bytes; 16-byte chunk c of
 // row r sits in slot c ^ ((r >> 1) & 7), which makes the 16-lane groups of a
 // ds_read_b128 hit 16 distinct bank units on gfx950's 64-bank LDS.
+// max of a value over the lane pair (l, l ^ 32), in every lane, without
+// LDS: v_permlane32_swap exchanges the upper half of one register with the
+// lower half of the other, so the two results hold each lane's own value
+// and its partner's.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <bool OUT_F32>
 __global__ __launch_bounds__(256) void attn_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -123,8 +135,12 @@ __global__ __launch_bounds__(256) void attn_kernel(
     wait_vm<0>();
   __syncthreads();
 
-  for (int kb = 0; kb < nkb; ++kb) {
-    const uint8_t* Ks = smem + (kb % kStages) * 2 * kTile;
+  // One 64-key block. The ring slot is a compile-time constant (the loop
+  // below is unrolled by kStages), so every LDS read address is a per-lane
+  // register plus an immediate offset.
+  auto block = [&](int kb, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    const uint8_t* Ks = smem + slot * 2 * kTile;
     const uint8_t* Vs = Ks + kTile;
     // all 16 fragments of the tile are read up front: the K reads feed the
     // score MFMAs, the V reads land while the softmax runs
@@ -169,7 +185,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[k2][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_halves(mx);
     // Lazy rescaling: the exponent reference m_run only moves (and O, l are
     // rescaled by 2^((m_old - m_new) c)) when some lane's max has grown by
     // more than 8 in the log2 domain; otherwise p = 2^(s c - m_run c) stays
@@ -222,9 +238,22 @@ __global__ __launch_bounds__(256) void attn_kernel(
       wait_vm<0>();
     __syncthreads();
     if (kb + kStages < nkb) issue(kb + kStages);
+  };
+  static_assert(kStages == 3, "the unrolled loop below walks 3 slots");
+  int kb = 0;
+  for (; kb + 2 < nkb; kb += 3) {
+    block(kb, std::integral_constant<int, 0>{});
+    block(kb + 1, std::integral_constant<int, 1>{});
+    block(kb + 2, std::integral_constant<int, 2>{});
   }
+  if (kb < nkb) block(kb, std::integral_constant<int, 0>{});
+  if (kb + 1 < nkb) block(kb + 1, std::integral_constant<int, 1>{});
 
-  l_run += __shfl_xor(l_run, 32, 64);
+  {
+    const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run),
+                                                      __float_as_uint(l_run), false, false);
+    l_run = __uint_as_float(sw2[0]) + __uint_as_float(sw2[1]);
+  }
   const float inv = 1.0f / l_run;
   const int q = q0 + l32;
   if (q >= T) return;
