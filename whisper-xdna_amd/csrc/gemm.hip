@@ -642,7 +642,15 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     wait_vmcnt<0>();
   __syncthreads();
   load_frags(0, 0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
+  // One K-step. ISSUE: refill the slot this step frees with step kt + S;
+  // NEXT: read step kt+1's first fragments. Both are compile-time, so each
+  // variant is one basic block the scheduling groups below can order: after
+  // the barrier the next step's first LDS reads go out first, then the DMA
+  // instructions alternate one-to-one with this step's last MFMAs, so the
+  // address unit drains the DMA while the matrix cores run (issued back to
+  // back, the DMA would hold the wave's MFMAs behind it).
+  auto step = [&](int kt, auto issue_c, auto next_c) {
+    constexpr bool ISSUE = decltype(issue_c)::value, NEXT = decltype(next_c)::value;
     static_for<KS - 1>([&](auto kk) {
       load_frags(kt, kk + 1, (kk + 1) & 1);
       mfmas(kk & 1);
@@ -652,17 +660,28 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     });
     // step kt+1 must have landed; issued so far are steps 0 .. kt+S-1, so the
     // S-2 steps after kt+1 may remain in flight (all of them near the end)
-    if (kt + C::S - 1 < nk)
+    if (ISSUE)
       wait_vmcnt<(C::S - 2) * C::IPS>();
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's reads done
     __syncthreads();
-    if (kt + C::S < nk) issue(kt + C::S);
-    if (kt + 1 < nk) load_frags(kt + 1, 0, 0);
+    if (NEXT) load_frags(kt + 1, 0, 0);
+    if (ISSUE) issue(kt + C::S);
     mfmas((KS - 1) & 1);
+    if (NEXT) __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+    static_for<C::IPS>([&](auto) {
+      if (ISSUE) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    });
     __builtin_amdgcn_sched_barrier(0);
-  }
+  };
+  using T_ = std::integral_constant<bool, true>;
+  using F_ = std::integral_constant<bool, false>;
+  int kt = 0;
+  for (; kt + C::S < nk; ++kt) step(kt, T_{}, T_{});
+  for (; kt + 1 < nk; ++kt) step(kt, F_{}, T_{});
+  if (kt < nk) step(kt, F_{}, F_{});
 
   store_tile_t<MODE, C::TM, C::TN>(e, acc, bv, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
 #endif
