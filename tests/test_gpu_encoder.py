@@ -7,8 +7,9 @@ Gates (cosine over all output elements, synthetic seeded inputs):
   large-v3 (32 layers, ctx 1500)     >= 0.994
   reduced context (ctx 512)          >= 0.9999
 Size-independent properties: batch item b of a batched forward equals the
-same mel run alone, bit for bit; graph replay equals eager launch, bit for
-bit, replay after replay.
+same mel run alone, bit for bit (for batch sizes that pick the same GEMM
+split, as batch 1 and 3 of tiny do); graph replay equals eager launch, bit
+for bit, replay after replay; split-K GEMMs are deterministic.
 """
 import numpy as np
 import pytest
@@ -25,6 +26,11 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(scope="module")
 def tiny():
     return synth.make_weights("tiny")
+
+
+@pytest.fixture(scope="module")
+def large():
+    return synth.make_weights("large-v3")
 
 
 def _enc(dev, W, **kw):
@@ -96,9 +102,9 @@ def test_small_encoder_cosine(dev):
     assert c >= 0.9999
 
 
-def test_large_v3_encoder_cosine(dev):
+def test_large_v3_encoder_cosine(dev, large):
     case("encoder large-v3 32 layers ctx 1500")
-    W = synth.make_weights("large-v3")
+    W = large
     mel = synth.make_mel(128, 3000, seed=0)
     got = _fwd(_enc(dev, W), mel, dev)
     ref = OE.encoder_torch(W, mel)
@@ -106,6 +112,29 @@ def test_large_v3_encoder_cosine(dev):
     report("large_v3_encoder", cosine=c, max_abs=float(np.abs(got - ref).max()))
     assert got.shape == (1500, 1280) and np.isfinite(got).all()
     assert c >= 0.994
+
+
+def test_split_k_batch1(dev, large, monkeypatch):
+    """At batch 1 the large-v3 fc2 (K 5120) and conv2 (K 3840) GEMMs have
+    120 output tiles of 128x128 and split K over two workgroups per tile.
+    The result does not depend on which workgroup of a tile finishes last
+    (partials summed in split order): two runs agree bit for bit. It agrees
+    with the unsplit GEMMs up to fp32 summation order, and with the oracle."""
+    case("encoder large-v3 2 layers batch 1: split-K determinism and parity")
+    mel = synth.make_mel(128, 3000, seed=3)
+    a = _fwd(_enc(dev, large, n_layer=2), mel, dev)
+    b = _fwd(_enc(dev, large, n_layer=2), mel, dev)
+    np.testing.assert_array_equal(a, b)
+    monkeypatch.setenv("WXH_GEMM_SPLITK", "1")
+    c = _fwd(_enc(dev, large, n_layer=2), mel, dev)
+    monkeypatch.delenv("WXH_GEMM_SPLITK")
+    ref = OE.encoder_torch(large, mel, n_layer=2)
+    c_split, c_plain = cosine(a, ref), cosine(c, ref)
+    report("split_k_batch1", cosine_split_vs_plain=cosine(a, c), cosine_split=c_split,
+           cosine_plain=c_plain, max_abs_split_vs_plain=float(np.abs(a - c).max()))
+    assert not np.array_equal(a, c), "WXH_GEMM_SPLITK=1 should change the summation order"
+    assert cosine(a, c) >= 0.99999
+    assert c_split >= 0.9999 and c_plain >= 0.9999
 
 
 def test_profile_stages(dev, tiny):

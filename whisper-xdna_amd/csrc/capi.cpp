@@ -332,6 +332,8 @@ struct wxh_encoder {
   uint16_t* vt = nullptr;    // [B*nh, 64, Tp]
   uint16_t* o = nullptr;     // [B*ctx, d]
   uint16_t* f = nullptr;     // [B*ctx, ffn]
+  float* sk_ws = nullptr;    // split-K partials (fixed size)
+  unsigned* sk_cnt = nullptr;  // split-K per-tile counters (zeroed, kept zeroed)
   std::vector<void*> ws_allocs;
   bool use_graph = true;
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
@@ -418,6 +420,9 @@ std::vector<std::string> required_names(const wxh_encoder_dims& d) {
   return v;
 }
 
+constexpr int64_t kSplitKElems = 512ll * 128 * 128;  // 32 MiB of fp32
+constexpr int kSplitKTiles = 512;
+
 int ensure_workspace(wxh_encoder* E, int batch, int frames) {
   const auto& D = E->dims;
   const int64_t B = batch, T = frames;
@@ -446,12 +451,23 @@ int ensure_workspace(wxh_encoder* E, int batch, int frames) {
   if (int r = dalloc(L, &E->vt, need_qkv, true)) return r;
   if (int r = dalloc(L, &E->o, need_x, true)) return r;
   if (int r = dalloc(L, &E->f, need_f, true)) return r;
+  if (int r = dalloc(L, &E->sk_ws, (size_t)kSplitKElems, false)) return r;
+  if (int r = dalloc(L, &E->sk_cnt, (size_t)kSplitKTiles, true)) return r;
   E->cap_mel = need_mel;
   E->cap_x1 = need_x1;
   E->cap_x = need_x;
   E->cap_qkv = need_qkv;
   E->cap_f = need_f;
   return WXH_OK;
+}
+
+// Split-K for the GEMMs whose tile count leaves CUs idle (batch 1-2): one
+// partial slice per split of C, at most 512 workgroups of 128x128 tiles.
+void set_splitk(wxh_encoder* E, wx::EpiParams& e) {
+  e.sk_ws = E->sk_ws;
+  e.sk_ws_elems = kSplitKElems;
+  e.sk_cnt = E->sk_cnt;
+  e.sk_cnt_len = kSplitKTiles;
 }
 
 // Zero rows 0 and T+1 of every batch item of the padded conv1 output (the
@@ -507,6 +523,7 @@ int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* t
     e.bias = E->conv2_b;
     e.aux = E->pos;
     e.rows_per_batch = ctx;
+    set_splitk(E, e);
     WXH_HIP(wx::launch_gemm(M, d, 3 * d, a, E->conv2_w, 3 * d, wx::EPI_CONV2, e, s));
     if (int r = mark(ST_CONV2)) return r;
   }
@@ -539,6 +556,7 @@ int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* t
       e.out = E->x;
       e.ldo = d;
       e.bias = W.bo;
+      set_splitk(E, e);
       WXH_HIP(wx::launch_gemm(M, d, d, a, W.wo, d, wx::EPI_RESID, e, s));
       if (int r = mark(ST_OUT)) return r;
     }
@@ -561,6 +579,7 @@ int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* t
       e.out = E->x;
       e.ldo = d;
       e.bias = W.b2;
+      set_splitk(E, e);
       WXH_HIP(wx::launch_gemm(M, d, E->ffn, a, W.w2, E->ffn, wx::EPI_RESID, e, s));
       if (int r = mark(ST_FC2)) return r;
     }

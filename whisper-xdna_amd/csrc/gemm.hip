@@ -522,6 +522,89 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Split-K partials. A wave's accumulators (the C^T layout of store_tile_t:
+// block (i, j) holds row row0 + 32 i + l % 32, columns col0 + 32 j + 8 g +
+// 4 (l / 32) + 0..3) go to / come from an fp32 [M][N] slice of the
+// workspace, rows and columns outside C skipped. The workgroups of one tile
+// may sit on different XCDs, whose L2s are not coherent with each other:
+// the partials are written and read with the sc1 cache policy (coherent at
+// device scope, through to memory), so no device-wide fence -- which on
+// this GPU writes back and invalidates the whole L2 -- is needed.
+constexpr int kCpolSc1 = 16;
+
+template <int TM, int TN>
+__device__ __forceinline__ void sk_store(__amdgpu_buffer_rsrc_t ws, int64_t base,
+                                         const f32x16 (&acc)[TM][TN], int M, int N, int row0,
+                                         int col0, int lane) {
+  const int l32 = lane & 31, half = lane >> 5;
+  static_for<TM>([&](auto i) {
+    const int m = row0 + i * 32 + l32;
+    if (m >= M) return;
+    const int64_t rb = base + (int64_t)m * N;
+    static_for<TN>([&](auto j) {
+      static_for<4>([&](auto g) {
+        const int n0 = col0 + j * 32 + g * 8 + half * 4;
+        if ((N & 3) == 0 && n0 + 3 < N) {
+          const f32x4 v = {acc[i][j][g * 4], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
+                           acc[i][j][g * 4 + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ws,
+                                                 (int)((rb + n0) * 4), 0, kCpolSc1);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n0 + r < N)
+              __builtin_amdgcn_raw_buffer_store_b32(
+                  __builtin_bit_cast(uint32_t, acc[i][j][g * 4 + r]), ws,
+                  (int)((rb + n0 + r) * 4), 0, kCpolSc1);
+        }
+      });
+    });
+  });
+}
+
+// acc <- sum over s = 0 .. splits-1 of partial s, added in that order (own
+// partial `me` taken from the registers: the same values), so the result
+// does not depend on which workgroup finished last.
+template <int TM, int TN>
+__device__ __forceinline__ void sk_reduce(__amdgpu_buffer_rsrc_t ws, int64_t slice, int splits,
+                                          int me, f32x16 (&acc)[TM][TN], int M, int N,
+                                          int row0, int col0, int lane) {
+  const int l32 = lane & 31, half = lane >> 5;
+  static_for<TM>([&](auto i) {
+    const int m = row0 + i * 32 + l32;
+    if (m >= M) return;
+    static_for<TN>([&](auto j) {
+      static_for<4>([&](auto g) {
+        const int n0 = col0 + j * 32 + g * 8 + half * 4;
+        if (n0 >= N) return;
+        const bool vec = (N & 3) == 0 && n0 + 3 < N;
+        const f32x4 own = {acc[i][j][g * 4], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
+                           acc[i][j][g * 4 + 3]};
+        f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < splits; ++s) {
+          f32x4 v = own;
+          if (s != me) {
+            const int64_t e0 = s * slice + (int64_t)m * N + n0;
+            if (vec) {
+              v = __builtin_bit_cast(
+                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(ws, (int)(e0 * 4), 0, kCpolSc1));
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                v[r] = n0 + r < N ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                 ws, (int)((e0 + r) * 4), 0, kCpolSc1))
+                                  : 0.f;
+            }
+          }
+          sum = s == 0 ? v : sum + v;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][g * 4 + r] = sum[r];
+      });
+    });
+  });
+}
+
 template <class C, int MODE>
 __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, GemmA a,
                                                          const uint16_t* __restrict__ W,
@@ -542,7 +625,13 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   const int l32 = lane & 31, half = lane >> 5;
 
   const int nm = (M + C::BM - 1) / C::BM, nn = (N + C::BN - 1) / C::BN;
-  const int pid = remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
+  // split-K: the `splits` workgroups of one tile are adjacent ids, each
+  // taking K / splits of the reduction
+  const int splits = e.splits;
+  const int split = splits > 1 ? (int)blockIdx.x % splits : 0;
+  const int tile_id = splits > 1 ? (int)blockIdx.x / splits : (int)blockIdx.x;
+  const int ksplit = K / splits, kbase = split * ksplit;
+  const int pid = remap ? xcd_remap(tile_id, nm * nn) : tile_id;
   const int width = group_m * nn;
   const int first_m = (pid / width) * group_m;
   const int gsz = min(nm - first_m, group_m);
@@ -576,7 +665,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   }
   auto issue = [&](int kt) {
     uint8_t* base = smem + (kt % C::S) * C::STAGE;
-    const int soff = kt * C::BK * 2;
+    const int soff = (kbase + kt * C::BK) * 2;
 #pragma unroll
     for (int j = 0; j < C::A_INSTR; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -599,7 +688,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   f32x4 bv[C::TN][4];
   load_bias<C::TN>(e.bias, N, bn0 + wn * C::WTN, lane, bv);
 
-  const int nk = K / C::BK;
+  const int nk = ksplit / C::BK;
   const int sw = (l32 / C::RPW) % C::CPR;  // the swizzle of every row this lane reads
   const int arow = (wm * C::WTM + l32) * C::ROWB;
   const int brow = (wn * C::WTN + l32) * C::ROWB;
@@ -683,6 +772,30 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   for (; kt + 1 < nk; ++kt) step(kt, F_{}, T_{});
   if (kt < nk) step(kt, F_{}, F_{});
 
+  if (splits > 1) {
+    // Publish this split's partial, then count the tile's finished splits;
+    // the last one sums them and runs the epilogue. No workgroup waits on
+    // another, so any dispatch order completes. The flag lives in the ring's
+    // first word: every LDS read and DMA of the main loop has completed
+    // before its last barrier.
+    int& sk_last = *reinterpret_cast<int*>(smem);
+    const int64_t slice = (int64_t)M * N;
+    const auto wsr = __builtin_amdgcn_make_buffer_rsrc(
+        e.sk_ws, (short)0, (int)(e.sk_ws_elems * 4), 0x00020000);
+    sk_store<C::TM, C::TN>(wsr, split * slice, acc, M, N, bm0 + wm * C::WTM,
+                           bn0 + wn * C::WTN, lane);
+    wait_vmcnt<0>();  // this thread's partial has reached the coherence point
+    __syncthreads();
+    if (tid == 0)
+      sk_last = __hip_atomic_fetch_add(e.sk_cnt + tile_id, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(splits - 1);
+    __syncthreads();
+    if (!sk_last) return;
+    sk_reduce<C::TM, C::TN>(wsr, slice, splits, split, acc, M, N, bm0 + wm * C::WTM,
+                            bn0 + wn * C::WTN, lane);
+    if (tid == 0)  // ready for the next launch
+      __hip_atomic_store(e.sk_cnt + tile_id, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   store_tile_t<MODE, C::TM, C::TN>(e, acc, bv, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
 #endif
 }
@@ -692,7 +805,7 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const uin
                                   int64_t ldw, int mode, const EpiParams& e,
                                   int a_bytes, int w_bytes, hipStream_t s) {
   const int tiles = ((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
-  dim3 grid(tiles), block(C::NT);
+  dim3 grid(tiles * e.splits), block(C::NT);
   // Tile order. Workgroups go to the 8 XCDs round-robin by id; with
   // `remap` each XCD instead walks its own contiguous run of the grouped
   // order, so the tiles one XCD runs at a time form a compact block (8 row
@@ -742,10 +855,33 @@ static int64_t a_extent_bytes(int M, int K, const GemmA& a) {
   return (hi + K) * 2;
 }
 
+// Split count for a launch of `tiles` 128x128 tiles at one workgroup per
+// CU: with fewer tiles than CUs, K is cut into the largest number of
+// 64-multiple pieces that keeps tiles x splits within the 256 CUs and each
+// piece at least 1536 long. Shorter pieces lose more to writing and reading
+// the partials than they gain (measured at batch 1: fc2, K 5120, 2 splits
+// 74 -> 47 us; out-proj, K 1280, 2 splits slower). WXH_GEMM_SPLITK=n
+// forces n (tuning sweeps; 1 disables).
+static int pick_splits(int M, int N, int K, int64_t tiles, const EpiParams& e) {
+  if (!e.sk_ws || !e.sk_cnt || tiles > e.sk_cnt_len) return 1;
+  auto fits = [&](int sp) {
+    return K % (sp * 64) == 0 && (int64_t)sp * M * N <= e.sk_ws_elems;
+  };
+  if (const char* f = getenv("WXH_GEMM_SPLITK")) {
+    const int sp = atoi(f);
+    return sp > 1 && fits(sp) ? sp : 1;
+  }
+  for (int sp = 4; sp >= 2; --sp)
+    if (tiles * sp <= 256 && K / sp >= 1536 && fits(sp)) return sp;
+  return 1;
+}
+
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
-                       int64_t ldw, int mode, const EpiParams& e,
+                       int64_t ldw, int mode, const EpiParams& e_in,
                        hipStream_t s) {
   if (M <= 0 || N <= 0) return hipSuccess;
+  EpiParams e = e_in;
+  e.splits = 1;
   const int64_t ab = a_extent_bytes(M, K, a);
   const int64_t wb = ((int64_t)(N - 1) * ldw + K) * 2;
   const bool dma = K > 0 && K % 64 == 0 && a.lda % 8 == 0 && ldw % 8 == 0 &&
@@ -761,12 +897,18 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   // the same bytes in the same time as the 2-slot BK 64 ring
   using T128k32s4 = DCfg<128, 128, 2, 2, 32, 4>;
   using T256w8k32s4 = DCfg<256, 256, 2, 4, 32, 4>;
+  using T128s3 = DCfg<128, 128, 2, 2, 64, 3>;
+  using T128s4 = DCfg<128, 128, 2, 2, 64, 4>;
+  const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
 #define WX_TRY(NAME, CFG)                                                              \
   if (f == NAME) {                                                                     \
     if (K % CFG::BK) return hipErrorInvalidValue;                                      \
+    if (CFG::BM == 128) e.splits = pick_splits(M, N, K, tiles128, e);                  \
     return gemm_dma_launch<CFG>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);     \
   }
   WX_TRY("128x128", T128)
+  WX_TRY("128x128s3", T128s3)
+  WX_TRY("128x128s4", T128s4)
   WX_TRY("256x256w8", T256w8)
   WX_TRY("128x128k32s4", T128k32s4)
   WX_TRY("256x256w8k32s4", T256w8k32s4)
@@ -779,6 +921,15 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
   if (big_tiles >= 256)
     return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  // At most one 128x128 tile per CU (batch 1-2: fc2, out-proj, conv2), the
+  // per-step time is the DMA latency: a 3-slot ring (one workgroup per CU)
+  // keeps two steps in flight (batch 1: fc2 74 -> 54 us, out-proj 27 -> 24),
+  // and split-K adds workgroups where K is long. With more tiles, two
+  // workgroups per CU on the 2-slot ring do better (batch 1 QKV 29 vs 37 us).
+  if (tiles128 <= 256) {
+    e.splits = pick_splits(M, N, K, tiles128, e);
+    return gemm_dma_launch<T128s3>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  }
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
 }
 

@@ -77,6 +77,17 @@ struct EpiParams {
   int n_head = 0;
   int t_pad = 0;                   // padded key length of Q/K/Vt
   int d_model = 0;
+  // Split-K workspace (optional). With it, launch_gemm may split K over
+  // `splits` workgroups per output tile when there are too few tiles to fill
+  // the GPU: each writes its fp32 partial to sk_ws ([splits][M][N]), and the
+  // last of a tile's workgroups to finish (per-tile counter in sk_cnt, which
+  // must start zeroed and is left zeroed) sums the partials in split order
+  // and runs the epilogue.
+  float* sk_ws = nullptr;
+  int64_t sk_ws_elems = 0;
+  unsigned* sk_cnt = nullptr;
+  int sk_cnt_len = 0;
+  int splits = 1;                  // set by launch_gemm
 };
 
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
