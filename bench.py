@@ -36,8 +36,8 @@ PEAK_HBM = 8.0e12       # MI355X HBM3E, B/s
 # by what it reads for a 512 MiB device copy (FETCH_SIZE x 2.000, WRITE_SIZE
 # x 1.000); the summaries, with their commands, are in profiles/.
 TRAFFIC_BYTES = {
-    "fc1": (1.0596e9, "profiles/gemm_fc1_l16_traffic.md"),
-    "attention": (2.503e8, "profiles/attention_l16_traffic.md"),
+    "fc1": (1.0689e9, "profiles/gemm_fc1_l16_traffic.md"),
+    "attention": (2.504e8, "profiles/attention_l16_traffic.md"),
 }
 LARGE = dict(n_mels=128, d=1280, n_head=20, n_layer=32, n_ctx=1500)
 WORKLOADS = {
