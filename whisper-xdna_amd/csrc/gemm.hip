@@ -605,6 +605,145 @@ __device__ __forceinline__ void sk_reduce(__amdgpu_buffer_rsrc_t ws, int64_t sli
   });
 }
 
+// Epilogues through LDS, for tiles wholly inside C. In registers a lane
+// holds 4-column runs of 32 different rows, so direct stores (and the fp32
+// residual's loads) hand the memory pipeline 32 separate 16-byte pieces per
+// instruction: ~10k cycles for a 256x256 bf16 tile and ~24k for the fp32
+// residual even when every line stays in L2. Instead the finished tile is
+// staged in the idle LDS ring and moved a row at a time, every memory
+// instruction covering whole contiguous rows. LDS layout: row r at r * ROWB,
+// 16-byte chunk q in slot q ^ (r % CPR), which keeps both the column-run
+// writes and the row reads within two-way bank conflicts. Activations that
+// make the epilogue VALU-bound (GELU) gain nothing here: the direct path
+// already hides its stores under the arithmetic.
+
+// bias + bf16 RNE of the wave's tile into LDS rows [wm * WTM, + WTM)
+template <class C>
+__device__ __forceinline__ void stage_bf16(const f32x16 (&acc)[C::TM][C::TN],
+                                           const f32x4 (&bv)[C::TN][4], uint8_t* smem, int wm,
+                                           int wn, int lane) {
+  constexpr int ROWB = C::BN * 2, CPR = ROWB / 16;
+  static_assert(C::BM * ROWB <= C::S * C::STAGE, "staged tile fits the ring");
+  const int l32 = lane & 31, half = lane >> 5;
+  static_for<C::TM>([&](auto i) {
+    const int r = wm * C::WTM + i * 32 + l32;
+    uint8_t* rowp = smem + r * ROWB + half * 8;
+    static_for<C::TN>([&](auto j) {
+      static_for<4>([&](auto g) {
+        const int q = (wn * C::WTN + j * 32 + g * 8) / 8;
+        const f32x4 x = {acc[i][j][g * 4] + bv[j][g][0], acc[i][j][g * 4 + 1] + bv[j][g][1],
+                         acc[i][j][g * 4 + 2] + bv[j][g][2], acc[i][j][g * 4 + 3] + bv[j][g][3]};
+        const u32x2 v = {f2bf2(x[0], x[1]), f2bf2(x[2], x[3])};
+        *reinterpret_cast<u32x2*>(rowp + ((q ^ (r % CPR)) << 4)) = v;
+      });
+    });
+  });
+}
+
+// plain bf16 C (EPI_BF16)
+template <class C>
+__device__ __forceinline__ void epi_lds_bf16(const EpiParams& e, const f32x16 (&acc)[C::TM][C::TN],
+                                             const f32x4 (&bv)[C::TN][4], uint8_t* smem,
+                                             int bm0, int bn0, int wm, int wn, int lane, int tid) {
+  constexpr int ROWB = C::BN * 2, CPR = ROWB / 16;
+  stage_bf16<C>(acc, bv, smem, wm, wn, lane);
+  __syncthreads();
+  constexpr int PER = C::BM * CPR / C::NT;
+  static_assert(PER * C::NT == C::BM * CPR, "whole chunks per thread");
+  uint16_t* out = static_cast<uint16_t*>(e.out);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int c = tid + k * C::NT;
+    const int r = c / CPR, ch = c % CPR;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * ROWB + ((ch ^ (r % CPR)) << 4));
+    *reinterpret_cast<u32x4*>(out + (int64_t)(bm0 + r) * e.ldo + bn0 + ch * 8) = v;
+  }
+}
+
+// Q or K column tile of the fused QKV GEMM: BN / 64 whole heads; row m =
+// (b, t) of head h goes to ((b * n_head + h) * t_pad + t) * 64, a 128-byte
+// run per head
+template <class C>
+__device__ __forceinline__ void epi_lds_qk(const EpiParams& e, const f32x16 (&acc)[C::TM][C::TN],
+                                           const f32x4 (&bv)[C::TN][4], uint8_t* smem, int bm0,
+                                           int bn0, int wm, int wn, int lane, int tid) {
+  constexpr int ROWB = C::BN * 2, CPR = ROWB / 16;
+  stage_bf16<C>(acc, bv, smem, wm, wn, lane);
+  __syncthreads();
+  const int wh = bn0 / e.d_model;
+  const int h0 = (bn0 - wh * e.d_model) >> 6;
+  uint16_t* base = wh == 0 ? e.q : e.k;
+  const int T = e.rows_per_batch;
+  constexpr int PER = C::BM * CPR / C::NT;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int c = tid + k * C::NT;
+    const int r = c / CPR, ch = c % CPR;
+    const int m = bm0 + r, b = m / T, t = m - b * T;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * ROWB + ((ch ^ (r % CPR)) << 4));
+    *reinterpret_cast<u32x4*>(base + (((int64_t)b * e.n_head + h0 + (ch >> 3)) * e.t_pad + t) * 64 +
+                              (ch & 7) * 8) = v;
+  }
+}
+
+// fp32 C (EPI_F32) or C += (EPI_RESID), one wave-row band of WTM rows at a
+// time (an fp32 256x256 tile is twice the ring): the band's waves stage
+// acc + bias, then every thread moves whole rows, residual loads issued
+// ahead of the LDS reads
+template <class C, int MODE>
+__device__ __forceinline__ void epi_lds_f32(const EpiParams& e, const f32x16 (&acc)[C::TM][C::TN],
+                                            const f32x4 (&bv)[C::TN][4], uint8_t* smem, int bm0,
+                                            int bn0, int wm, int wn, int lane, int tid) {
+  constexpr int ROWB = C::BN * 4, CPR = ROWB / 16;
+  static_assert(C::WTM * ROWB <= C::S * C::STAGE, "staged band fits the ring");
+  constexpr int PER = C::WTM * CPR / C::NT;
+  static_assert(PER * C::NT == C::WTM * CPR, "whole chunks per thread");
+  constexpr int BATCH = PER < 8 ? PER : 8;
+  static_assert(PER % BATCH == 0, "batches");
+  const int l32 = lane & 31, half = lane >> 5;
+  float* out = static_cast<float*>(e.out);
+  static_for<C::WM>([&](auto ph) {
+    if (wm == ph) {
+      static_for<C::TM>([&](auto i) {
+        const int r = i * 32 + l32;
+        uint8_t* rowp = smem + r * ROWB;
+        static_for<C::TN>([&](auto j) {
+          static_for<4>([&](auto g) {
+            const int q = (wn * C::WTN + j * 32 + g * 8 + half * 4) / 4;
+            const f32x4 x = {acc[i][j][g * 4] + bv[j][g][0], acc[i][j][g * 4 + 1] + bv[j][g][1],
+                             acc[i][j][g * 4 + 2] + bv[j][g][2],
+                             acc[i][j][g * 4 + 3] + bv[j][g][3]};
+            *reinterpret_cast<f32x4*>(rowp + ((q ^ (r % CPR)) << 4)) = x;
+          });
+        });
+      });
+    }
+    __syncthreads();
+    const int rb = bm0 + ph * C::WTM;
+#pragma unroll
+    for (int k0 = 0; k0 < PER; k0 += BATCH) {
+      f32x4 xr[BATCH];
+      if (MODE == EPI_RESID) {
+#pragma unroll
+        for (int k = 0; k < BATCH; ++k) {
+          const int c = tid + (k0 + k) * C::NT;
+          const int r = c / CPR, ch = c % CPR;
+          xr[k] = *reinterpret_cast<const f32x4*>(out + (int64_t)(rb + r) * e.ldo + bn0 + ch * 4);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) {
+        const int c = tid + (k0 + k) * C::NT;
+        const int r = c / CPR, ch = c % CPR;
+        f32x4 v = *reinterpret_cast<const f32x4*>(smem + r * ROWB + ((ch ^ (r % CPR)) << 4));
+        if (MODE == EPI_RESID) v += xr[k];
+        *reinterpret_cast<f32x4*>(out + (int64_t)(rb + r) * e.ldo + bn0 + ch * 4) = v;
+      }
+    }
+    if (ph + 1 < C::WM) __syncthreads();  // the next band reuses the ring
+  });
+}
+
 template <class C, int MODE>
 __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, GemmA a,
                                                          const uint16_t* __restrict__ W,
@@ -790,11 +929,36 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
       sk_last = __hip_atomic_fetch_add(e.sk_cnt + tile_id, 1u, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(splits - 1);
     __syncthreads();
-    if (!sk_last) return;
+    const bool last = sk_last;
+    __syncthreads();  // every wave has read the flag before the epilogue reuses LDS
+    if (!last) return;
     sk_reduce<C::TM, C::TN>(wsr, slice, splits, split, acc, M, N, bm0 + wm * C::WTM,
                             bn0 + wn * C::WTN, lane);
     if (tid == 0)  // ready for the next launch
       __hip_atomic_store(e.sk_cnt + tile_id, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // Staged epilogues (conditions uniform over the workgroup; the ring is
+  // idle once every wave is past the main loop's last barrier: DMA drained,
+  // fragment reads done).
+  if (bm0 + C::BM <= M && bn0 + C::BN <= N) {
+    if constexpr (MODE == EPI_BF16) {
+      if ((e.ldo & 7) == 0 && ((uintptr_t)e.out & 15) == 0) {
+        epi_lds_bf16<C>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
+        return;
+      }
+    }
+    if constexpr (MODE == EPI_QKV) {
+      if (bn0 < 2 * e.d_model && e.d_model % C::BN == 0) {
+        epi_lds_qk<C>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
+        return;
+      }
+    }
+    if constexpr (MODE == EPI_F32 || MODE == EPI_RESID) {
+      if ((e.ldo & 3) == 0 && ((uintptr_t)e.out & 15) == 0) {
+        epi_lds_f32<C, MODE>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
+        return;
+      }
+    }
   }
   store_tile_t<MODE, C::TM, C::TN>(e, acc, bv, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
 #endif
