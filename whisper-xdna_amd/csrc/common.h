@@ -88,22 +88,22 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
 // has relative error < 2.8e-4, far below a bf16 ulp (2^-8 relative); fp32
 // evaluation over 4M inputs (the tail included) is within 1 bf16 ulp of
 // the exact GELU. The exponent is taken as 2^(arg + 32) and the 2^-33 is
-// applied by the last multiply, so results in fp32's denormal range come out
-// of an IEEE multiply instead of an exp2 that may flush them. |x| >= 16
-// returns relu(x) (|GELU - relu| < 1e-55 there), which also maps +-inf.
-// One reciprocal, one exp2 and 12 other VALU operations.
+// applied by the final FMA, so results in fp32's denormal range come out of
+// an IEEE operation instead of an exp2 that may flush them. In terms of x:
+// t = 1 / (1 + |x| / (2 sqrt2)) and z^2 log2 e = x^2 (log2 e / 2). For
+// |x| >= 14 the exp2 underflows to 0 and the result is relu(x) exactly; x
+// enters the product clamped to [-16, 16], so +-inf (t = 0) map to relu
+// too. One reciprocal, one exp2 and 11 other VALU operations.
 __device__ __forceinline__ float gelu_erf(float x) {
-  constexpr float kL2e = 1.4426950408889634f;
-  const float z = fabsf(x) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  constexpr float kHalfL2e = 0.72134752044448170f;  // log2(e) / 2
+  const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), 0.35355339059327376f, 1.0f));
   float p = -0.5002267360687256f;
   p = fmaf(p, t, 0.9977306127548218f);
   p = fmaf(p, t, 1.31719970703125f);
   p = fmaf(p, t, -1.8143213987350464f + 32.0f);
-  const float e = __builtin_amdgcn_exp2f(fmaf(-z, z * kL2e, p));
-  const float q = (x * t) * e * 1.1641532182693481e-10f;  // 2^-33
-  const float g = fmaxf(x, 0.f) - fabsf(q);
-  return fabsf(x) < 16.0f ? g : fmaxf(x, 0.f);
+  const float e = __builtin_amdgcn_exp2f(fmaf(x * x, -kHalfL2e, p));
+  const float w = __builtin_amdgcn_fmed3f(x, -16.0f, 16.0f) * t * e;  // q 2^33
+  return fmaf(-fabsf(w), 1.1641532182693481e-10f, fmaxf(x, 0.f));  // 2^-33
 }
 
 // poly4 GELU constants: kernels/gelu_poly4_coeffs.h:4-13 (all bf16-exact;
