@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace wx {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -78,6 +80,18 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
                     : tall * per + (xcd - tall) * (per - 1) + local;
 }
 
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i in [0, N). Keeps
+// every accumulator index a constant whatever the unroller decides, so the
+// accumulators never get dynamically indexed (which would spill them).
+template <class F, int... Is>
+__device__ __forceinline__ void sfor_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  sfor_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // erf-GELU, GELU(x) = x Phi(x), for every kernel that applies it (row
 // kernel and GEMM epilogues). With z = |x| / sqrt2 and t = 1 / (1 + z/2):

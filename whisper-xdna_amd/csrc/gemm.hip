@@ -45,18 +45,6 @@ struct Cfg {
   static constexpr int LDS_BYTES = 2 * (BM + BN) * LDK * 2;
 };
 
-// Compile-time loop: f(std::integral_constant<int, i>) for i in [0, N). Keeps
-// every accumulator index a constant whatever the unroller decides, so the
-// accumulators never get dynamically indexed (which would spill them).
-template <class F, int... Is>
-__device__ __forceinline__ void sfor_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  sfor_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // Write one wave's TM x TN grid of 32x32 accumulator blocks through the
 // epilogue. Block (i, j) covers rows row0 + 32 i .. and columns col0 + 32 j ..;
 // lane l holds column l % 32 and rows 8 g + 4 (l / 32) + r (g, r < 4). Row-
