@@ -752,13 +752,17 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   const int l32 = lane & 31, half = lane >> 5;
 
   const int nm = (M + C::BM - 1) / C::BM, nn = (N + C::BN - 1) / C::BN;
-  // split-K: the `splits` workgroups of one tile are adjacent ids, each
-  // taking K / splits of the reduction
+  // split-K: workgroup `pid` takes split pid / tiles of tile pid % tiles,
+  // i.e. K / splits of the reduction; with the XCD-contiguous order each XCD
+  // then walks a compact block of tiles within one split, sharing its A rows
+  // and W columns in L2
   const int splits = e.splits;
-  const int split = splits > 1 ? (int)blockIdx.x % splits : 0;
-  const int tile_id = splits > 1 ? (int)blockIdx.x / splits : (int)blockIdx.x;
+  const int ntiles = nm * nn;
+  const int gid = remap ? xcd_remap(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+  const int split = splits > 1 ? gid / ntiles : 0;
+  const int tile_id = splits > 1 ? gid - split * ntiles : gid;
   const int ksplit = K / splits, kbase = split * ksplit;
-  const int pid = remap ? xcd_remap(tile_id, nm * nn) : tile_id;
+  const int pid = tile_id;
   const int width = group_m * nn;
   const int first_m = (pid / width) * group_m;
   const int gsz = min(nm - first_m, group_m);
