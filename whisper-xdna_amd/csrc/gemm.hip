@@ -1054,6 +1054,7 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   using T128k32s4 = DCfg<128, 128, 2, 2, 32, 4>;
   using T256w8k32s4 = DCfg<256, 256, 2, 4, 32, 4>;
   using T128s3 = DCfg<128, 128, 2, 2, 64, 3>;
+  using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
   using T128s4 = DCfg<128, 128, 2, 2, 64, 4>;
   const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
 #define WX_TRY(NAME, CFG)                                                              \
@@ -1084,7 +1085,7 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   // workgroups per CU on the 2-slot ring do better (batch 1 QKV 29 vs 37 us).
   if (tiles128 <= 256) {
     e.splits = pick_splits(M, N, K, tiles128, e);
-    return gemm_dma_launch<T128s3>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+    return gemm_dma_launch<T128w8s3>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
   }
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
 }
