@@ -102,6 +102,26 @@ def test_gemm_bf16_and_gelu_epilogues(dev):
     np.testing.assert_array_equal(yp, OR.gelu_poly4(acc, "rne", f32_input=True))
 
 
+def test_gemm_256_tiles_gelu_and_bf16(dev):
+    """An fc1-sized GEMM on the 256x256 tile: 24 x 20 tiles, the last row
+    tile partial (checked epilogue) and the others interior (the GELU
+    epilogue stores directly, the plain bf16 one through LDS). The main loop
+    is the same for every epilogue, so the fp32 accumulator is the
+    reference for both; two launches in a row agree."""
+    M, N, K = 6100, 5120, 1280
+    case(f"gemm 256x256 gelu/bf16 M={M} N={N} K={K}")
+    A, W, b = _operands(M, N, K, seed=9)
+    a, w, bb = _dev(A, dev), _dev(W, dev), _dev(b, dev, False)
+    acc = dev.gemm(a, w, bb, L.WXH_EPI_F32).cpu().numpy()
+    rows = np.r_[np.random.default_rng(2).choice(M - 300, 40, replace=False), np.arange(M - 260, M, 13)]
+    ref, mag = _exact(A[rows], W, b)
+    assert (np.abs(acc[rows] - ref) <= 2e-4 * mag + 1e-6).all()
+    yg = bits(dev.gemm(a, w, bb, L.WXH_EPI_BF16_GELU_ERF))
+    assert OB.ulp_diff(yg, OB.round_rne(OR.gelu_erf(acc).astype(np.float32))).max() <= 1
+    np.testing.assert_array_equal(bits(dev.gemm(a, w, bb, L.WXH_EPI_BF16_GELU_ERF)), yg)
+    np.testing.assert_array_equal(bits(dev.gemm(a, w, bb, L.WXH_EPI_BF16)), OB.round_rne(acc))
+
+
 def test_gemm_residual_epilogue(dev):
     M, N, K = 1500, 1280, 5120
     case(f"gemm residual M={M} N={N} K={K}")
