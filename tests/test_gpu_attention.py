@@ -41,9 +41,15 @@ def _run(dev, q, k, v, nh, scale, out_dtype=torch.float32):
     return dev.attention(Q, K, Vt, B, nh, T, scale, out_dtype=out_dtype).cpu().float().numpy().reshape(B, T, d)
 
 
-@pytest.mark.parametrize("B,T,nh", [(1, 1500, 20), (2, 512, 6), (1, 100, 2), (3, 65, 1), (1, 1, 1)])
-def test_attention_vs_closed_form(dev, B, T, nh):
-    case(f"attention B={B} T={T} nh={nh}")
+# Fewer than 256 workgroups (every shape but the batch-4 one) split each
+# workgroup's keys over two wave groups; "nosplit" forces the one-part kernel.
+@pytest.mark.parametrize("B,T,nh,mode", [(1, 1500, 20, ""), (2, 512, 6, ""), (1, 100, 2, ""),
+                                         (3, 65, 1, ""), (1, 1, 1, ""), (4, 1500, 20, ""),
+                                         (1, 1500, 20, "nosplit"), (3, 65, 1, "nosplit")])
+def test_attention_vs_closed_form(dev, B, T, nh, mode, monkeypatch):
+    case(f"attention B={B} T={T} nh={nh} {mode}")
+    if mode == "nosplit":
+        monkeypatch.setenv("WXH_ATTN_NOSPLIT", "1")
     rng = np.random.default_rng(T + nh)
     d = nh * 64
     q, k, v = (OB.rb(rng.normal(0, 1, (B, T, d)).astype(np.float32)) for _ in range(3))

@@ -58,13 +58,17 @@ __device__ __forceinline__ float max_halves(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <bool OUT_F32>
-__global__ __launch_bounds__(256) void attn_kernel(
+// KSPLIT = 2 (few workgroups, e.g. batch 1): 8 waves, the first 4 take the
+// first half of the key blocks and the other 4 the second half, for the same
+// 4 x 32 queries, each half through its own ring; the halves' (O, max, sum)
+// are combined through LDS at the end.
+template <bool OUT_F32, int KSPLIT>
+__global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ Vt, int n_head, int T, int Tp,
     float scale_log2, void* __restrict__ O, int64_t ldo) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * 2 * kTile];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[KSPLIT * kStages * 2 * kTile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -73,6 +77,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
   // wave index: uniform across the wave; readfirstlane makes that visible
   // to the compiler, so everything derived from it stays in SGPRs
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qg = w & 3, kh = w >> 2;  // query group, key part
   // the query blocks of one head run on one XCD, which then fetches that
   // head's K and Vt into its L2 once instead of once per XCD
   const int nqb = gridDim.x;
@@ -81,32 +86,40 @@ __global__ __launch_bounds__(256) void attn_kernel(
   const int qb = pid % nqb;
   const int h = (pid / nqb) % n_head, b = pid / (nqb * n_head);
   const int64_t bh = (int64_t)b * n_head + h;
-  const int q0 = qb * kQB + w * 32;
+  const int q0 = qb * kQB + qg * 32;
   const uint16_t* Qh = Q + bh * Tp * kHeadDim;
   const uint16_t* Kh = K + bh * Tp * kHeadDim;
   const uint16_t* Vh = Vt + bh * kHeadDim * Tp;
   const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, Tp * kHeadDim * 2, 0x00020000);
   const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vh, (short)0, kHeadDim * Tp * 2, 0x00020000);
 
-  // DMA: wave w moves tile rows 16 w .. 16 w + 15 of both tiles
+  // DMA: wave qg of a part moves tile rows 16 qg .. 16 qg + 15 of both tiles
   const int lrow = lane >> 3;
   uint32_t koff[2], voff[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int row = (w * 2 + j) * 8 + lrow;
+    const int row = (qg * 2 + j) * 8 + lrow;
     const int lchunk = (lane & 7) ^ ((row >> 1) & 7);
     koff[j] = (uint32_t)((row * kHeadDim + lchunk * 8) * 2);
     voff[j] = (uint32_t)((row * Tp + lchunk * 8) * 2);
   }
-  auto issue = [&](int kb) {
-    uint8_t* base = smem + (kb % kStages) * 2 * kTile;
+  // key blocks of this part: [kbeg, kbeg + nkb); every wave runs nb trips
+  // (one barrier each), a part with fewer blocks idles through the last
+  const int nkb_all = Tp / kKB;
+  const int nb = (nkb_all + KSPLIT - 1) / KSPLIT;
+  const int kbeg = kh * nb;
+  const int nkb = max(0, min(nkb_all, kbeg + nb) - kbeg);
+  uint8_t* ring = smem + kh * (kStages * 2 * kTile);
+  auto issue = [&](int i) {  // the part's i-th block into slot i % kStages
+    uint8_t* base = ring + (i % kStages) * 2 * kTile;
+    const int kb = kbeg + i;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(base + (w * 2 + j) * 1024), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(base + (qg * 2 + j) * 1024), 16,
                                                koff[j], kb * kKB * kHeadDim * 2, 0, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(base + kTile + (w * 2 + j) * 1024),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(base + kTile + (qg * 2 + j) * 1024),
                                                16, voff[j], kb * kKB * 2, 0, 0);
   };
 
@@ -125,7 +138,6 @@ __global__ __launch_bounds__(256) void attn_kernel(
   float m_run = -INFINITY, l_run = 0.f;
   const int sw = (l32 >> 1) & 7;  // the swizzle of every row this lane reads
 
-  const int nkb = Tp / kKB;
 #pragma unroll
   for (int st = 0; st < kStages; ++st)
     if (st < nkb) issue(st);
@@ -138,9 +150,15 @@ __global__ __launch_bounds__(256) void attn_kernel(
   // One 64-key block. The ring slot is a compile-time constant (the loop
   // below is unrolled by kStages), so every LDS read address is a per-lane
   // register plus an immediate offset.
-  auto block = [&](int kb, auto slot_c) {
+  auto block = [&](int i, auto slot_c) {
+    if (i >= nkb) {  // this part has run out of blocks: keep the barrier count
+      wait_vm<0>();
+      __syncthreads();
+      return;
+    }
+    const int kb = kbeg + i;
     constexpr int slot = decltype(slot_c)::value;
-    const uint8_t* Ks = smem + slot * 2 * kTile;
+    const uint8_t* Ks = ring + slot * 2 * kTile;
     const uint8_t* Vs = Ks + kTile;
     // all 16 fragments of the tile are read up front: the K reads feed the
     // score MFMAs, the V reads land while the softmax runs
@@ -232,27 +250,52 @@ __global__ __launch_bounds__(256) void attn_kernel(
     }
     // tile kb+1 must have landed (the stages after it may still fly); every
     // wave is done with slot kb once past the barrier, which it then refills
-    if (kb + kStages - 1 < nkb)
+    if (i + kStages - 1 < nkb)
       wait_vm<(kStages - 2) * 4>();
     else
       wait_vm<0>();
     __syncthreads();
-    if (kb + kStages < nkb) issue(kb + kStages);
+    if (i + kStages < nkb) issue(i + kStages);
   };
   static_assert(kStages == 3, "the unrolled loop below walks 3 slots");
-  int kb = 0;
-  for (; kb + 2 < nkb; kb += 3) {
-    block(kb, std::integral_constant<int, 0>{});
-    block(kb + 1, std::integral_constant<int, 1>{});
-    block(kb + 2, std::integral_constant<int, 2>{});
+  int i = 0;
+  for (; i + 2 < nb; i += 3) {
+    block(i, std::integral_constant<int, 0>{});
+    block(i + 1, std::integral_constant<int, 1>{});
+    block(i + 2, std::integral_constant<int, 2>{});
   }
-  if (kb < nkb) block(kb, std::integral_constant<int, 0>{});
-  if (kb + 1 < nkb) block(kb + 1, std::integral_constant<int, 1>{});
+  if (i < nb) block(i, std::integral_constant<int, 0>{});
+  if (i + 1 < nb) block(i + 1, std::integral_constant<int, 1>{});
 
   {
     const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run),
                                                       __float_as_uint(l_run), false, false);
     l_run = __uint_as_float(sw2[0]) + __uint_as_float(sw2[1]);
+  }
+  if constexpr (KSPLIT == 2) {
+    // The second part hands (O, max, sum) to the first through LDS (idle:
+    // every part's last trip waited for its DMA before the last barrier):
+    // O = O0 2^((m0-m)c) + O1 2^((m1-m)c), l likewise, m = max(m0, m1).
+    float* xs = reinterpret_cast<float*>(smem) + qg * (34 * 64) + lane;
+    if (kh == 1) {
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xs[(db * 16 + r) * 64] = o[db][r];
+      xs[32 * 64] = m_run;
+      xs[33 * 64] = l_run;
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    const float m1 = xs[32 * 64], l1 = xs[33 * 64];
+    const float mm = fmaxf(m_run, m1);
+    const float a0 = __builtin_amdgcn_exp2f((m_run - mm) * scale_log2);
+    const float a1 = __builtin_amdgcn_exp2f((m1 - mm) * scale_log2);
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * a0 + xs[(db * 16 + r) * 64] * a1;
+    l_run = l_run * a0 + l1 * a1;
   }
   const float inv = 1.0f / l_run;
   const int q = q0 + l32;
@@ -284,10 +327,19 @@ hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
   const int Tp = attn_padded_len(T);
   dim3 grid((T + kQB - 1) / kQB, n_head, batch);
   const float scale_log2 = scale * 1.4426950408889634f;
+  // Fewer workgroups than CUs (batch 1: 20 heads x 12 query blocks): split
+  // every workgroup's keys over twice the waves, halving each wave's walk.
+  if ((int64_t)grid.x * grid.y * grid.z < 256 && getenv("WXH_ATTN_NOSPLIT") == nullptr) {
+    if (o_dtype == DT_F32)
+      attn_kernel<true, 2><<<grid, 512, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
+    else
+      attn_kernel<false, 2><<<grid, 512, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
+    return hipGetLastError();
+  }
   if (o_dtype == DT_F32)
-    attn_kernel<true><<<grid, 256, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
+    attn_kernel<true, 1><<<grid, 256, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
   else
-    attn_kernel<false><<<grid, 256, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
+    attn_kernel<false, 1><<<grid, 256, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
   return hipGetLastError();
 }
 
