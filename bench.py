@@ -30,6 +30,7 @@ sys.path[:0] = [str(ROOT / "whisper-xdna_amd"), str(ROOT)]
 METRIC = "large-v3 encoder ms @ctx=1500 bs=1; mel-frames/s bs=16; % bf16 MFMA peak"
 PEAK_BF16 = 2.5e15      # MI355X dense bf16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12       # MI355X HBM3E, B/s
+PEAK_FP64_TF = 78.6     # MI355X fp64, TFLOP/s
 # HBM-side bytes per launch of the kernels that can be the dominant stage,
 # measured with `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over
 # whisper-xdna_amd/wxhip/probe.py at the batch-16 shape, each counter scaled
@@ -149,6 +150,33 @@ def rowop_bandwidth(dev):
     return out
 
 
+def frontend_rate(dev, batch, n_mels):
+    """GPU log-mel front end (wxh_log_mel) over `batch` synthetic 30 s clips:
+    device time per launch (HIP events over 20 launches). Work: a 201-bin
+    real DFT of 3000 frames of 400 samples per clip, in fp64 (199 paired
+    terms x 2 FMA per bin, the algorithmic count of a direct real DFT; the
+    Goertzel recurrence the kernel runs takes 1.5x that), plus the filterbank."""
+    import torch
+    g = torch.Generator(device=dev.device).manual_seed(0)
+    audio = torch.randn(batch, 480000, generator=g, device=dev.device) * 0.1
+    out = torch.empty(batch, n_mels, 3000, dtype=torch.float32, device=dev.device)
+    for _ in range(3):
+        dev.log_mel(audio, n_mels, out=out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        dev.log_mel(audio, n_mels, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / 20
+    flop = batch * 3000 * (201 * 199 * 4 + 2 * 2 * 201)
+    return {"batch": batch, "n_mels": n_mels, "us": round(us, 1),
+            "us_per_clip": round(us / batch, 2), "clips_per_s": round(batch / us * 1e6, 1),
+            "fp64_tflops": round(flop / us / 1e6, 2),
+            "fp64_frac": round(flop / us / 1e6 / PEAK_FP64_TF, 4)}
+
+
 def cpu_baseline(W, n_mels):
     """torch fp32 oracle on this host's cores: one warmup and two timed
     forwards of one large-v3 sample (3000 mel frames)."""
@@ -165,7 +193,16 @@ def cpu_baseline(W, n_mels):
         OE.encoder_torch(W, mel)
         ts.append(time.perf_counter() - t0)
     t = float(np.median(ts))
+    # the front end on the CPU: the oracle's numpy log-mel of one 30 s clip
+    from oracle import audio as OA
+    clip = np.random.default_rng(0).normal(0, 0.1, 480000).astype(np.float32)
+    OA.log_mel_spectrogram(clip, n_mels)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        OA.log_mel_spectrogram(clip, n_mels)
+    fe_ms = (time.perf_counter() - t0) / 3 * 1e3
     return {"value": round(3000 / t, 1), "unit": "mel-frames/s",
+            "frontend_log_mel_ms_per_clip": round(fe_ms, 2),
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": "1 of the 16 large-v3 mels (3000 frames, batch 1), torch fp32 "
                       "encoder restatement, median of 2 after 1 warmup",
@@ -266,6 +303,8 @@ def main():
     elif args.workload == "l1":
         res["latency_bs1_ms"] = round(dt * 1e3, 3)
 
+    res["frontend"] = frontend_rate(dev, B, 128)
+    log(f"frontend: {res['frontend']}")
     if not args.no_rowops:
         res["rowops"] = rowop_bandwidth(dev)
         log(f"rowops: {res['rowops']}")

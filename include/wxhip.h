@@ -63,7 +63,8 @@ enum {
   WXH_FAIL_GEMM = 1u << 0,
   WXH_FAIL_ATTN = 1u << 1,
   WXH_FAIL_ROWOP = 1u << 2,
-  WXH_FAIL_ENCODER = 1u << 3
+  WXH_FAIL_ENCODER = 1u << 3,
+  WXH_FAIL_FRONTEND = 1u << 4
 };
 
 /* ------------------------------------------------------------------ context */
@@ -94,6 +95,32 @@ int wxh_get_stream(wxh_ctx* ctx, void** stream);
 /* Block until all work on the context's stream is done. Replaces the
  * reference's run waits (rawxrt.py:319-324, r.wait(RUN_TIMEOUT_MS)). */
 int wxh_synchronize(wxh_ctx* ctx);
+
+/* --------------------------------------------------------------- front end */
+
+/* Log-mel spectrogram of 16 kHz mono audio: whisper's front end, which the
+ * reference runs on the CPU through openai-whisper's log_mel_spectrogram
+ * (tools/dump_ref.py:55-57, serve/npu_stt_server.py:334-336,
+ * bench/probe_int8_decode.py:128). Centred frames of 400 samples every 160
+ * (reflect padding at both ends, the last frame dropped), periodic Hann
+ * window, power of the 201 DFT bins, Slaney mel filterbank
+ * (librosa.filters.mel(16000, 400, n_mels)), log10(max(., 1e-10)) floored at
+ * the clip's maximum - 8, then (x + 4) / 4.
+ * audio: device fp32 [batch][n_samples], n_samples >= 400 (30 s windows are
+ * 480000: whisper's pad_or_trim is the caller's, as in the reference);
+ * out: device fp32 [batch][n_mels][n_samples / 160], the encoder's mel
+ * input. The floor is taken per clip (the reference converts one window at a
+ * time). The filterbank of each n_mels, and a small scratch for the clip
+ * maxima (64 ints per clip, grown to the largest batch), are allocated on
+ * first use and kept by the context, so calls on one context must not
+ * overlap in time. Fail-inject bit WXH_FAIL_FRONTEND. */
+int wxh_log_mel(wxh_ctx* ctx, const float* audio, int batch, int n_samples, int n_mels,
+                float* out, void* stream);
+
+/* Host-side: the mel filterbank wxh_log_mel applies, [n_mels][201] float32
+ * into `out` (host memory), as librosa.filters.mel(16000, 400, n_mels)
+ * builds it. Needs no GPU. */
+int wxh_mel_filterbank(int n_mels, float* out);
 
 /* ------------------------------------------------------------------ row ops */
 

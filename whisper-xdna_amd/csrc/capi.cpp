@@ -64,6 +64,9 @@ struct wxh_ctx {
   hipStream_t stream = nullptr;
   uint32_t fail_mask = 0;
   std::atomic<int> refs{1};
+  std::map<int, uint8_t*> logmel;  // n_mels -> device constants (log-mel front end)
+  int* logmel_slots = nullptr;     // per-clip maxima scratch of wxh_log_mel
+  int logmel_cap = 0;              // clips it holds
 };
 
 namespace {
@@ -119,6 +122,8 @@ void ctx_release(wxh_ctx* c) {
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   (void)hipStreamDestroy(c->stream);
+  for (auto& kv : c->logmel) (void)hipFree(kv.second);
+  if (c->logmel_slots) (void)hipFree(c->logmel_slots);
   delete c;
 }
 }  // namespace
@@ -210,6 +215,48 @@ int wxh_convert_f32_bf16(wxh_ctx* c, const float* x, int64_t ldx, uint16_t* y,
                   ldy >= (transpose ? rows : cols),
               "wxh_convert_f32_bf16: bad arguments");
   WXH_HIP(wx::launch_convert(x, ldx, y, ldy, rows, cols, transpose != 0, pick(c, stream)));
+  return WXH_OK;
+}
+
+// ------------------------------------------------------------- front end
+
+int wxh_log_mel(wxh_ctx* c, const float* audio, int batch, int n_samples, int n_mels,
+                float* out, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_FRONTEND, "wxh_log_mel")) return r;
+  WXH_REQUIRE(audio && out, "wxh_log_mel: null pointer");
+  WXH_REQUIRE(batch >= 0 && n_samples >= 400 && n_mels > 0 && n_mels <= 256,
+              "wxh_log_mel: batch=%d n_samples=%d n_mels=%d", batch, n_samples, n_mels);
+  auto it = c->logmel.find(n_mels);
+  if (it == c->logmel.end()) {
+    const std::vector<uint8_t> h = wx::logmel_constants(n_mels);
+    uint8_t* d = nullptr;
+    WXH_HIP(hipMalloc(&d, h.size()));
+    hipError_t e = hipMemcpy(d, h.data(), h.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(d);
+      return fail(WXH_ERR_HIP, "wxh_log_mel: hipMemcpy: %s", hipGetErrorString(e));
+    }
+    it = c->logmel.emplace(n_mels, d).first;
+  }
+  if (batch > c->logmel_cap) {
+    if (c->logmel_slots) {
+      WXH_HIP(hipDeviceSynchronize());  // an earlier call may still use it
+      (void)hipFree(c->logmel_slots);
+      c->logmel_slots = nullptr;
+      c->logmel_cap = 0;
+    }
+    WXH_HIP(hipMalloc(&c->logmel_slots, (size_t)batch * wx::kLogMelSlots * sizeof(int)));
+    c->logmel_cap = batch;
+  }
+  WXH_HIP(wx::launch_log_mel(audio, batch, n_samples, n_mels, it->second, out,
+                             c->logmel_slots, pick(c, stream)));
+  return WXH_OK;
+}
+
+int wxh_mel_filterbank(int n_mels, float* out) {
+  WXH_REQUIRE(out && n_mels > 0 && n_mels <= 256, "wxh_mel_filterbank: n_mels=%d", n_mels);
+  const std::vector<float> w = wx::mel_filterbank(n_mels);
+  std::memcpy(out, w.data(), w.size() * sizeof(float));
   return WXH_OK;
 }
 

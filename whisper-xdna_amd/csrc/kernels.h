@@ -5,6 +5,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <vector>
 #include <stdint.h>
 
 namespace wx {
@@ -127,6 +129,15 @@ hipError_t launch_pack_qkv(const float* q, const float* k, const float* v,
 // ---------------------------------------------------------------- encoder
 // mel fp32 [B, C, T] -> bf16 [B, T + 2, C] with zero rows 0 and T + 1: the
 // conv1 im2col becomes a window of 3 consecutive rows.
+// whisper log-mel front end (audio.hip): `consts` from logmel_constants()
+// on the device; out [batch][n_mels][n_samples / 160]; slots: device int
+// scratch of kLogMelSlots per clip (the clip maxima), overwritten
+constexpr int kLogMelSlots = 64;
+std::vector<uint8_t> logmel_constants(int n_mels);
+std::vector<float> mel_filterbank(int n_mels);
+hipError_t launch_log_mel(const float* audio, int batch, int n_samples, int n_mels,
+                          const uint8_t* consts, float* out, int* slots, hipStream_t s);
+
 hipError_t launch_prep_mel(const float* mel, int batch, int C, int T,
                            uint16_t* out, hipStream_t s);
 

@@ -9,6 +9,7 @@ libwxhip.so, hand-written HIP kernels driven through a C ABI (include/wxhip.h).
   wxhip.rowops    the row-op surface of src/rowops.py + compile_rowop.py codes
   wxhip.native    HipEncoder: the device-resident, hipGraph-replayed forward
   wxhip.device    Device: every kernel on torch device tensors
+  wxhip.audio     WAV input and the log-mel front end (whisper names), on the GPU
   wxhip.synth     seeded synthetic weights / mels / row-op inputs
 """
 from . import _lib

@@ -18,6 +18,7 @@ WXH_GELU_ERF, WXH_GELU_POLY4_RNE, WXH_GELU_POLY4_TRUNC = 0, 1, 2
 WXH_EPI_F32, WXH_EPI_BF16, WXH_EPI_BF16_GELU_ERF = 0, 1, 2
 WXH_EPI_BF16_GELU_POLY4, WXH_EPI_RESID_F32 = 3, 4
 WXH_FAIL_GEMM, WXH_FAIL_ATTN, WXH_FAIL_ROWOP, WXH_FAIL_ENCODER = 1, 2, 4, 8
+WXH_FAIL_FRONTEND = 16
 
 ERROR_NAMES = {1: "invalid argument", 2: "HIP error", 3: "injected failure",
                4: "unsupported", 5: "bad state"}
@@ -52,6 +53,8 @@ SIGNATURES = {
     "wxh_set_fail_inject": [P, U32],
     "wxh_get_stream": [P, PP],
     "wxh_synchronize": [P],
+    "wxh_log_mel": [P, P, I, I, I, P, P],
+    "wxh_mel_filterbank": [I, P],
     "wxh_layernorm": [P, P, I, I64, P, I64, P, I64, P, P, F, P, I, I64, I, I, P],
     "wxh_gelu": [P, P, I, I64, P, I64, I, I, I, P],
     "wxh_softmax_rows": [P, P, I64, P, I64, I, I, P],

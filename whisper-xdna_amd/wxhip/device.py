@@ -122,6 +122,23 @@ class Device:
                _ld(y), rows, cols, variant, self.stream())
         return y
 
+    def log_mel(self, audio, n_mels=80, out=None):
+        """Whisper log-mel features of 16 kHz fp32 audio on the device:
+        [n_samples] -> [n_mels, n_samples // 160], or [B, n_samples] ->
+        [B, n_mels, n_samples // 160] (floor at each clip's maximum - 8)."""
+        torch = _torch()
+        squeeze = audio.dim() == 1
+        a = (audio[None] if squeeze else audio)
+        self._check(a, torch.float32, "audio", 2)
+        a = a.contiguous()
+        B, n = a.shape
+        y = out if out is not None else torch.empty(B, n_mels, n // 160, dtype=torch.float32,
+                                                    device=self.device)
+        if tuple(y.shape) != (B, n_mels, n // 160) or y.dtype != torch.float32 or not y.is_contiguous():
+            raise ValueError(f"out must be contiguous fp32 [{B}, {n_mels}, {n // 160}]")
+        L.call("wxh_log_mel", self._h, _ptr(a), B, n, n_mels, _ptr(y), self.stream())
+        return y[0] if squeeze else y
+
     def softmax_rows(self, x, valid=None, out=None):
         """Row softmax of bf16 x over its first `valid` columns -> bf16."""
         torch = _torch()

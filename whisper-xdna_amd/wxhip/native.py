@@ -92,6 +92,13 @@ class HipEncoder:
                C.c_void_p(out.data_ptr()), self.dev.stream())
         return out[0] if squeeze else out
 
+    def forward_audio(self, audio, out=None):
+        """16 kHz fp32 audio on the device, [B, n_samples] or [n_samples]
+        (30 s windows: 480000 samples) -> features, with the log-mel front end
+        on the GPU as well (Device.log_mel with this model's n_mels)."""
+        mel = self.dev.log_mel(audio, self.n_mels)
+        return self.forward(mel, out=out)
+
     def forward_numpy(self, mel):
         """Host fp32 mel [B, n_mels, T] or [n_mels, T] -> host fp32 features."""
         m = np.ascontiguousarray(mel, dtype=np.float32)
