@@ -110,3 +110,29 @@ def test_audio_to_features_end_to_end(dev):
         c = cosine(got[b], ref)
         report("audio_to_features_tiny", clip=b, cosine=c)
         assert c >= 0.9999
+
+
+def test_encode_recording_batches_windows(dev):
+    """A 65 s recording at audio_ctx 500 (rung 512): three 30 s windows (the
+    last 5 s), log-mel and encoder each in one batch, equal to running the
+    windows one by one, and to the oracle front end + oracle encoder."""
+    import wxhip
+    from wxhip import windows as WN
+    case("encode_recording 65 s, ctx 512 (tiny)")
+    W = synth.make_weights("tiny")
+    enc = wxhip.HipEncoder(dev, W)
+    rng = np.random.default_rng(11)
+    t = np.arange(65 * 16000) / 16000
+    audio = (0.2 * np.sin(2 * np.pi * (200 + 30 * t) * t) + rng.normal(0, 0.03, t.size)).astype(np.float32)
+    feats, ctx = WN.encode_recording(enc, audio, audio_ctx=500)
+    assert ctx == 512 and tuple(feats.shape) == (3, 512, 384)
+    got = feats.cpu().numpy()
+    for i, (off, n) in enumerate(WN.split_windows(audio.size)):
+        win = OA.pad_or_trim(audio[off:off + n])
+        mel = dev.log_mel(torch.from_numpy(win).to(dev.device), 80)[None, :, :1024].contiguous()
+        one = enc.forward(mel).cpu().numpy()[0]
+        assert cosine(got[i], one) >= 0.99999
+        ref = OE.encoder_torch(W, OA.log_mel_spectrogram(win, 80)[:, :1024])
+        c = cosine(got[i], ref)
+        report("encode_recording_tiny", window=i, cosine=c)
+        assert c >= 0.9999

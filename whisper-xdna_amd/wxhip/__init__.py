@@ -10,6 +10,7 @@ libwxhip.so, hand-written HIP kernels driven through a C ABI (include/wxhip.h).
   wxhip.native    HipEncoder: the device-resident, hipGraph-replayed forward
   wxhip.device    Device: every kernel on torch device tensors
   wxhip.audio     WAV input and the log-mel front end (whisper names), on the GPU
+  wxhip.windows   audio_ctx ladder and 30 s windows of long recordings, batched
   wxhip.synth     seeded synthetic weights / mels / row-op inputs
 """
 from . import _lib
