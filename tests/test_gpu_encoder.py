@@ -221,3 +221,19 @@ def test_context_released_before_encoder(tiny):
     after = _fwd(enc, mel, own)
     np.testing.assert_array_equal(before, after)
     enc.close()                      # last holder: the context is freed here
+
+
+def test_encoder_from_ref_npz(dev, tiny, tmp_path):
+    """HipEncoder.from_file on a dump_ref.py-format .npz gives the same
+    device weights, hence the same features bit for bit, as the in-memory
+    dict; its stored mel goes through unchanged."""
+    import wxhip
+    from wxhip import weights as WT
+    case("encoder from ref.npz (tiny)")
+    mel = synth.make_mel(80, 3000, seed=4)
+    p = tmp_path / "ref_tiny.npz"
+    WT.save_ref_npz(p, tiny, mel=mel)
+    W2, mel2, _ = WT.load_ref_npz(p)
+    a = _fwd(_enc(dev, tiny), mel, dev)
+    b = _fwd(wxhip.HipEncoder.from_file(dev, p), mel2, dev)
+    np.testing.assert_array_equal(a, b)

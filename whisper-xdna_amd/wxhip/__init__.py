@@ -11,6 +11,7 @@ libwxhip.so, hand-written HIP kernels driven through a C ABI (include/wxhip.h).
   wxhip.device    Device: every kernel on torch device tensors
   wxhip.audio     WAV input and the log-mel front end (whisper names), on the GPU
   wxhip.windows   audio_ctx ladder and 30 s windows of long recordings, batched
+  wxhip.weights   weights from dump_ref.py .npz files and openai-whisper checkpoints
   wxhip.synth     seeded synthetic weights / mels / row-op inputs
 """
 from . import _lib

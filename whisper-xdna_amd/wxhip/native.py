@@ -92,6 +92,13 @@ class HipEncoder:
                C.c_void_p(out.data_ptr()), self.dev.stream())
         return out[0] if squeeze else out
 
+    @classmethod
+    def from_file(cls, dev, path, **kw):
+        """Weights from a dump_ref.py ``.npz`` or an openai-whisper checkpoint
+        (wxhip.weights), uploaded once as device bf16."""
+        from . import weights
+        return cls(dev, weights.load(path), **kw)
+
     def forward_audio(self, audio, out=None):
         """16 kHz fp32 audio on the device, [B, n_samples] or [n_samples]
         (30 s windows: 480000 samples) -> features, with the log-mel front end
