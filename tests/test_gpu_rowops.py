@@ -136,12 +136,42 @@ def test_gelu_poly4_f32_input_band(dev, inputs):
     assert (got[:, :1280] == 0).all() and (got[:, 2560:] == 0).all()
 
 
-def test_gelu_odd_width_scalar_path(dev):
-    case("gelu erf odd width 13x37")
+@pytest.mark.parametrize("variant", ["erf", "g4r", "g4"])
+def test_gelu_odd_width_scalar_path(dev, variant):
+    """Widths and strides that are not multiples of 8 take the one-element
+    path (with its own copy of the poly4 table)."""
+    case(f"gelu {variant} odd width 13x37")
     rng = np.random.default_rng(5)
     x = OB.rb(rng.normal(0, 3, (13, 37)).astype(np.float32))
-    y = dev.gelu(to_dev_bf16(x, dev), L.WXH_GELU_ERF)
-    assert _ulps(bits(y), OR.gelu_erf(x)).max() <= ULP
+    code = {"erf": L.WXH_GELU_ERF, "g4r": L.WXH_GELU_POLY4_RNE,
+            "g4": L.WXH_GELU_POLY4_TRUNC}[variant]
+    y = dev.gelu(to_dev_bf16(x, dev), code)
+    if variant == "erf":
+        assert _ulps(bits(y), OR.gelu_erf(x)).max() <= ULP
+    else:
+        np.testing.assert_array_equal(bits(y), OR.gelu_poly4(x, mode="rne" if variant == "g4r" else "trunc"))
+
+
+def test_gelu_strided_bands_and_tiny_inputs(dev):
+    """Row-strided input and output (the 32-bit chunk-index path) on values
+    around the poly4 table's ends: 0, denormals, 2^-10 and its neighbours,
+    the breaks 1, 2, 4 and beyond."""
+    case("gelu strided bands, table ends")
+    pts = np.array([0.0, 1e-40, 1e-30, 2.0 ** -11, 2.0 ** -10, 2.0 ** -10 * 1.0078125,
+                    2.0 ** -9, 0.5, 0.99609375, 1.0, 1.9921875, 2.0, 3.984375, 4.0,
+                    4.03125, 7.0, 1e4], np.float32)
+    row = OB.rb(np.concatenate([pts, -pts, np.linspace(-6, 6, 1024 - 2 * pts.size)]).astype(np.float32))
+    x = np.tile(row, (24, 1))
+    xd = torch.zeros(24, 1032, dtype=torch.bfloat16, device=dev.device)
+    xd[:, 8:1032] = to_dev_bf16(x, dev)
+    for variant, mode in ((L.WXH_GELU_POLY4_RNE, "rne"), (L.WXH_GELU_POLY4_TRUNC, "trunc")):
+        out = torch.zeros(24, 1040, dtype=torch.bfloat16, device=dev.device)
+        dev.gelu(xd[:, 8:1032], variant, out=out[:, 16:1040])
+        np.testing.assert_array_equal(bits(out)[:, 16:], OR.gelu_poly4(x, mode=mode))
+        assert (bits(out)[:, :16] == 0).all()
+    out = torch.zeros(24, 1040, dtype=torch.bfloat16, device=dev.device)
+    dev.gelu(xd[:, 8:1032], L.WXH_GELU_ERF, out=out[:, 16:1040])
+    assert _ulps(bits(out)[:, 16:], OR.gelu_erf(x)).max() <= ULP
 
 
 def test_softmax_rowop_shape(dev, inputs):

@@ -52,16 +52,36 @@ __device__ __forceinline__ float rb_trunc(float f) {
   return __uint_as_float(__float_as_uint(f) & 0xFFFF0000u);
 }
 
+// Full-wave reductions, result wave-uniform. Four in-row DPP steps (quad
+// swaps of 1 and 2 lanes, half-row mirror, row mirror) leave every lane of a
+// 16-lane row with the row's value; the four rows' values are read with
+// v_readlane and combined in scalar order. No LDS round trip on the path.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppRowMirror = 0x140;  // row_mirror
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  v += dpp_f<kDppQuadSwap1>(v);
+  v += dpp_f<kDppQuadSwap2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppRowMirror>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  v = fmaxf(v, dpp_f<kDppQuadSwap1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadSwap2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each
@@ -131,15 +151,15 @@ constexpr float kP4Coef[3][5] = {
 
 // GELU(x) = relu(x) + q(|x|) with q the 3-piece degree-4 bump, rounded to
 // bf16 at exactly the points gelu_poly4_eval.inc rounds. x must already be
-// bf16-exact. Returns the fp32 sum before the final rounding.
+// bf16-exact. poly4_q(s) is the bump for s = |x|; poly4_gelu_pre returns the
+// fp32 sum before the final rounding.
 // gelu_poly4_eval.inc evaluates the pieces p = 2, 1, 0 in turn and keeps the
 // last one whose break exceeds s; that is the smallest p with s < break[p]
 // (none for s >= 4 or NaN: q = 0). Only that piece is evaluated here, with
 // its constants picked by two compares; the arithmetic on it is unchanged,
 // so the result is bit-identical.
 template <bool RNE>
-__device__ __forceinline__ float poly4_gelu_pre(float x) {
-  const float s = fabsf(x);
+__device__ __forceinline__ float poly4_q(float s) {
   const bool in0 = s < 1.0f, in1 = s < 2.0f, in2 = s < 4.0f;
   // piece p's constant: kP4Coef[p][k] etc., selected without indexing (an
   // indexed constant array would be read from memory per element)
@@ -155,8 +175,12 @@ __device__ __forceinline__ float poly4_gelu_pre(float x) {
     // ah * u is exact in fp32 (two bf16 factors), so one rounding
     acc = fmaf(ah, u, sel(kP4Coef[0][k], kP4Coef[1][k], kP4Coef[2][k]));
   }
-  const float q = in2 ? (RNE ? rb_rne(acc) : rb_trunc(acc)) : 0.f;
-  return fmaxf(x, 0.f) + q;
+  return in2 ? (RNE ? rb_rne(acc) : rb_trunc(acc)) : 0.f;
+}
+
+template <bool RNE>
+__device__ __forceinline__ float poly4_gelu_pre(float x) {
+  return fmaxf(x, 0.f) + poly4_q<RNE>(fabsf(x));
 }
 
 }  // namespace wx

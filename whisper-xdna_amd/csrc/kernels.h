@@ -17,14 +17,19 @@ enum Gelu { GELU_NONE = -1, GELU_ERF = 0, GELU_POLY4_RNE = 1, GELU_POLY4_TRUNC =
 // ---------------------------------------------------------------- row ops
 // y = LN(x [+ resid]) * gamma + beta over each row of `cols` elements.
 // sum_out (fp32, optional) receives x + resid before normalisation.
+// stream: non-temporal loads and stores (for rows nothing reads again soon).
 hipError_t launch_layernorm(const void* x, int x_dtype, int64_t ldx,
                             const float* resid, int64_t ldr, float* sum_out,
                             int64_t lds, const float* gamma, const float* beta,
                             float eps, void* y, int y_dtype, int64_t ldy,
-                            int rows, int cols, hipStream_t s);
+                            int rows, int cols, bool stream, hipStream_t s);
 
 // Max row width the one-wave-per-row LayerNorm and softmax keep in registers.
 constexpr int kMaxRowCols = 4096;
+
+// Device tables the row kernels read (the poly4 GELU's q by bit pattern),
+// written on `s`; run once per device before the first row-kernel launch.
+hipError_t init_rowop_tables(hipStream_t s);
 
 // Element-wise GELU over a rows x cols band; y is bf16.
 hipError_t launch_gelu(const void* x, int x_dtype, int64_t ldx, uint16_t* y,

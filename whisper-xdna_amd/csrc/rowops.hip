@@ -16,86 +16,113 @@
 // All of these are HBM-bound: one read and one write of each element. The
 // row kernels put one wave on one row and keep the row in registers, so the
 // reductions are wave shuffles and each element is read once.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace wx {
 
 // ======================================================== LayerNorm
-// One wave per row; lane l owns 8-element chunks l, l+64, ... of the row.
-template <int MAXCH, bool XF32, bool YF32, bool RESID>
-__global__ __launch_bounds__(256) void ln_kernel(
-    const void* __restrict__ xp, int64_t ldx, const float* __restrict__ rp,
-    int64_t ldr, float* __restrict__ sp, int64_t lds,
-    const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
-    void* __restrict__ yp, int64_t ldy, int rows, int cols) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+// One wave per row; lane l owns 8-element chunks l, l+64, ... of the row
+// (NCH = chunks per lane, the row width rounded up to 512). A wave walks
+// rows row0, row0 + waves, ...: the next row's loads are issued before the
+// current row's reductions, so each wave keeps a row in flight while it
+// computes. gamma and beta (or 1 and 0) sit in LDS, loaded once per
+// workgroup. STREAM puts the non-temporal hint on the row loads and the
+// output stores (standalone calls: nothing reads the rows again soon).
+template <int NCH, bool XF32, bool RESID, bool STREAM>
+struct LnRow {
+  u32x4 x[NCH][XF32 ? 2 : 1];
+  u32x4 r[NCH][RESID ? 2 : 1];
+  // Every chunk slot is loaded through a descriptor that covers exactly the
+  // row (row is wave-uniform), so slots past the row read zeros instead of
+  // faulting: the loads are unconditional and their count is the same on
+  // every path, which lets the next row's loads stay in flight.
+  // A row outside [0, rows) gets an empty descriptor: its loads return
+  // zeros without touching memory, and are still issued.
+  // cols4 = the row's width in fp32 bytes (4 cols), computed once by the
+  // kernel in scalar registers
+  __device__ __forceinline__ void load(const void* xp, int64_t ldx, const float* rp,
+                                       int64_t ldr, int row, int rows, int lane, int cols4) {
+    constexpr int esz = XF32 ? 4 : 2;
+    constexpr int aux = STREAM ? 2 : 0;  // cache-policy bit 1: non-temporal
+    const bool in = row < rows;
+    row = in ? row : 0;
+    const int nx = in ? (XF32 ? cols4 : cols4 >> 1) : 0;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(xp) + row * ldx * esz), (short)0, nx,
+        0x00020000);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int h = 0; h < (XF32 ? 2 : 1); ++h)
+        x[c][h] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + c * 64) * 8 * esz + h * 16,
+                                                        0, aux);
+    if (RESID) {
+      const int nr = in ? cols4 : 0;
+      const auto rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rp + row * ldr),
+                                                        (short)0, nr, 0x00020000);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          r[c][RESID ? h : 0] =
+              __builtin_amdgcn_raw_buffer_load_b128(rr, (lane + c * 64) * 32 + h * 16, 0, aux);
+    }
+  }
+};
+
+// LayerNorm of one row from its loaded chunks; gb = gamma [cols], beta [cols]
+template <int NCH, bool XF32, bool YF32, bool RESID, bool STREAM>
+__device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cur,
+                                       const float* gb, float* __restrict__ sp, int64_t lds,
+                                       float eps, void* __restrict__ yp, int64_t ldy, int row,
+                                       int lane, int cols) {
+  auto st = [](auto v, auto* p) {
+    if (STREAM) __builtin_nontemporal_store(v, p); else *p = v;
+  };
   const int nch = cols >> 3;
-  float v[MAXCH][8];
-  float sum = 0.f;
-  // gamma and beta do not depend on the row: their loads are issued first so
-  // that their latency overlaps the row load and the two reductions
-  f32x4 gb[MAXCH][4];
-#pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
-    const int64_t col = (int64_t)(lane + c * 64) * 8;
-    const bool ok = lane + c * 64 < nch;
-    gb[c][0] = gb[c][1] = f32x4{1.f, 1.f, 1.f, 1.f};
-    gb[c][2] = gb[c][3] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (ok && gamma) {
-      gb[c][0] = *reinterpret_cast<const f32x4*>(gamma + col);
-      gb[c][1] = *reinterpret_cast<const f32x4*>(gamma + col + 4);
-    }
-    if (ok && beta) {
-      gb[c][2] = *reinterpret_cast<const f32x4*>(beta + col);
-      gb[c][3] = *reinterpret_cast<const f32x4*>(beta + col + 4);
-    }
-  }
-#pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
-    const int ch = lane + c * 64;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[c][j] = 0.f;
-    if (ch < nch) {
-      const int64_t col = (int64_t)ch * 8;
-      if (XF32) {
-        const float* x = static_cast<const float*>(xp) + row * ldx + col;
-        f32x4 a = *reinterpret_cast<const f32x4*>(x);
-        f32x4 b = *reinterpret_cast<const f32x4*>(x + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { v[c][j] = a[j]; v[c][j + 4] = b[j]; }
-      } else {
-        const uint16_t* x = static_cast<const uint16_t*>(xp) + row * ldx + col;
-        u16x8 a = *reinterpret_cast<const u16x8*>(x);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[c][j] = bf2f(a[j]);
-      }
-      if (RESID) {
-        const float* r = rp + row * ldr + col;
-        f32x4 a = *reinterpret_cast<const f32x4*>(r);
-        f32x4 b = *reinterpret_cast<const f32x4*>(r + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { v[c][j] += a[j]; v[c][j + 4] += b[j]; }
-        if (sp) {
-          float* o = sp + row * lds + col;
-          f32x4 lo = {v[c][0], v[c][1], v[c][2], v[c][3]};
-          f32x4 hi = {v[c][4], v[c][5], v[c][6], v[c][7]};
-          *reinterpret_cast<f32x4*>(o) = lo;
-          *reinterpret_cast<f32x4*>(o + 4) = hi;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sum += v[c][j];
-    }
-  }
   const float inv_n = 1.0f / (float)cols;
+  float v[NCH][8];
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int ch = lane + c * 64;
+    if (XF32) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[c][j] = __uint_as_float(cur.x[c][0][j]);
+        v[c][j + 4] = __uint_as_float(cur.x[c][XF32 ? 1 : 0][j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[c][2 * j] = __uint_as_float(cur.x[c][0][j] << 16);
+        v[c][2 * j + 1] = __uint_as_float(cur.x[c][0][j] & 0xFFFF0000u);
+      }
+    }
+    if (RESID) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[c][j] += __uint_as_float(cur.r[c][0][j]);
+        v[c][j + 4] += __uint_as_float(cur.r[c][RESID ? 1 : 0][j]);
+      }
+      if (sp && ch < nch) {
+        float* o = sp + row * lds + (int64_t)ch * 8;
+        st(f32x4{v[c][0], v[c][1], v[c][2], v[c][3]}, reinterpret_cast<f32x4*>(o));
+        st(f32x4{v[c][4], v[c][5], v[c][6], v[c][7]}, reinterpret_cast<f32x4*>(o + 4));
+      }
+    }
+    // slots past the row loaded zeros: they add nothing to the sum
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += v[c][j];
+  }
   const float mean = wave_sum(sum) * inv_n;
   // second pass over the registers: exact two-pass variance
   float sq = 0.f;
 #pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
+  for (int c = 0; c < NCH; ++c) {
     if (lane + c * 64 < nch) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -107,12 +134,14 @@ __global__ __launch_bounds__(256) void ln_kernel(
   const float var = wave_sum(sq) * inv_n;
   const float rstd = 1.0f / sqrtf(var + eps);
 #pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
+  for (int c = 0; c < NCH; ++c) {
     const int ch = lane + c * 64;
     if (ch >= nch) continue;
     const int64_t col = (int64_t)ch * 8;
+    const f32x4* g = reinterpret_cast<const f32x4*>(gb + col);
+    const f32x4* bb = reinterpret_cast<const f32x4*>(gb + cols + col);
+    const f32x4 g0 = g[0], g1 = g[1], b0 = bb[0], b1 = bb[1];
     float o[8];
-    const f32x4 g0 = gb[c][0], g1 = gb[c][1], b0 = gb[c][2], b1 = gb[c][3];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       o[j] = (v[c][j] - mean) * rstd * g0[j] + b0[j];
@@ -120,33 +149,99 @@ __global__ __launch_bounds__(256) void ln_kernel(
     }
     if (YF32) {
       float* y = static_cast<float*>(yp) + row * ldy + col;
-      f32x4 lo = {o[0], o[1], o[2], o[3]};
-      f32x4 hi = {o[4], o[5], o[6], o[7]};
-      *reinterpret_cast<f32x4*>(y) = lo;
-      *reinterpret_cast<f32x4*>(y + 4) = hi;
+      st(f32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<f32x4*>(y));
+      st(f32x4{o[4], o[5], o[6], o[7]}, reinterpret_cast<f32x4*>(y + 4));
     } else {
       uint16_t* y = static_cast<uint16_t*>(yp) + row * ldy + col;
-      u32x4 pk = {f2bf2(o[0], o[1]), f2bf2(o[2], o[3]), f2bf2(o[4], o[5]),
-                  f2bf2(o[6], o[7])};
-      *reinterpret_cast<u32x4*>(y) = pk;
+      st(u32x4{f2bf2(o[0], o[1]), f2bf2(o[2], o[3]), f2bf2(o[4], o[5]), f2bf2(o[6], o[7])},
+         reinterpret_cast<u32x4*>(y));
     }
   }
 }
 
-template <int MAXCH>
+template <int NCH, bool XF32, bool YF32, bool RESID, bool STREAM>
+__global__ __launch_bounds__(256) void ln_kernel(
+    const void* __restrict__ xp, int64_t ldx, const float* __restrict__ rp,
+    int64_t ldr, float* __restrict__ sp, int64_t lds,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
+    void* __restrict__ yp, int64_t ldy, int rows, int cols) {
+  extern __shared__ __align__(16) float ln_gb[];  // gamma [cols], beta [cols]
+  // wave-uniform; readfirstlane keeps it (and the descriptor lengths made
+  // from it) in scalar registers: cols is also read in the divergent loop
+  // below, after which the compiler would hold it in a VGPR
+  const int cols4 = __builtin_amdgcn_readfirstlane(cols * 4);
+  const int lane = threadIdx.x & 63;
+  const int row0 = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int waves = gridDim.x * 4;
+  // two row buffers in turn (no register copies, which would wait for the
+  // loads in flight); the first row's loads go out before gamma and beta
+  // are fetched, so the two trips to memory overlap
+  LnRow<NCH, XF32, RESID, STREAM> ra, rb;
+  int row = row0;
+  ra.load(xp, ldx, rp, ldr, row, rows, lane, cols4);
+  {
+    // gamma and beta as 16-byte pieces (cols <= 4096: at most 4 per thread),
+    // every load issued before the LDS writes
+    // (unconditional buffer loads: past the end, or for a null gamma or
+    // beta, they read zeros; a null gamma then becomes ones)
+    constexpr int kPer = kMaxRowCols / 4 / 256;
+    const int n4 = cols >> 2;
+    const auto rg = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(gamma), (short)0,
+                                                      gamma ? cols4 : 0, 0x00020000);
+    const auto rb2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(beta), (short)0,
+                                                       beta ? cols4 : 0, 0x00020000);
+    u32x4 g[kPer], b[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int off = (threadIdx.x + k * 256) * 16;
+      g[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0);
+      b[k] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = threadIdx.x + k * 256;
+      if (i < n4) {
+        reinterpret_cast<u32x4*>(ln_gb)[i] =
+            gamma ? g[k] : u32x4{0x3f800000u, 0x3f800000u, 0x3f800000u, 0x3f800000u};
+        reinterpret_cast<u32x4*>(ln_gb + cols)[i] = b[k];
+      }
+    }
+  }
+  __syncthreads();
+  while (row < rows) {
+    rb.load(xp, ldx, rp, ldr, row + waves, rows, lane, cols4);
+    ln_row<NCH, XF32, YF32, RESID, STREAM>(ra, ln_gb, sp, lds, eps, yp, ldy, row, lane, cols);
+    row += waves;
+    if (row >= rows) break;
+    ra.load(xp, ldx, rp, ldr, row + waves, rows, lane, cols4);
+    ln_row<NCH, XF32, YF32, RESID, STREAM>(rb, ln_gb, sp, lds, eps, yp, ldy, row, lane, cols);
+    row += waves;
+  }
+}
+
+// Workgroups at most: 2048 waves, each walking ~rows / 2048 rows with the
+// next row in flight (512 measured best at the encoder's [24000, 1280]).
+constexpr int kLnGrid = 512;
+
+template <int NCH>
 static hipError_t ln_dispatch(const void* x, int x_dtype, int64_t ldx,
                               const float* resid, int64_t ldr, float* sum_out,
                               int64_t lds, const float* gamma,
                               const float* beta, float eps, void* y,
                               int y_dtype, int64_t ldy, int rows, int cols,
-                              hipStream_t s) {
-  dim3 grid((rows + 3) / 4), block(256);
+                              bool stream, hipStream_t s) {
+  dim3 grid(std::min((rows + 3) / 4, kLnGrid)), block(256);
+  const size_t smem = 2 * (size_t)cols * sizeof(float);
   const bool xf = x_dtype == DT_F32, yf = y_dtype == DT_F32, r = resid != nullptr;
-#define WX_LN(XF, YF, R)                                                      \
-  if (xf == XF && yf == YF && r == R) {                                       \
-    ln_kernel<MAXCH, XF, YF, R><<<grid, block, 0, s>>>(                       \
-        x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols); \
-    return hipGetLastError();                                                 \
+#define WX_LN(XF, YF, R)                                                             \
+  if (xf == XF && yf == YF && r == R) {                                              \
+    if (stream)                                                                      \
+      ln_kernel<NCH, XF, YF, R, true><<<grid, block, smem, s>>>(                     \
+          x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols);   \
+    else                                                                             \
+      ln_kernel<NCH, XF, YF, R, false><<<grid, block, smem, s>>>(                    \
+          x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols);   \
+    return hipGetLastError();                                                        \
   }
   WX_LN(false, false, false) WX_LN(false, true, false)
   WX_LN(true, false, false) WX_LN(true, true, false)
@@ -160,58 +255,153 @@ hipError_t launch_layernorm(const void* x, int x_dtype, int64_t ldx,
                             const float* resid, int64_t ldr, float* sum_out,
                             int64_t lds, const float* gamma, const float* beta,
                             float eps, void* y, int y_dtype, int64_t ldy,
-                            int rows, int cols, hipStream_t s) {
+                            int rows, int cols, bool stream, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  if (cols <= 1024)
-    return ln_dispatch<2>(x, x_dtype, ldx, resid, ldr, sum_out, lds, gamma,
-                          beta, eps, y, y_dtype, ldy, rows, cols, s);
-  if (cols <= 2048)
-    return ln_dispatch<4>(x, x_dtype, ldx, resid, ldr, sum_out, lds, gamma,
-                          beta, eps, y, y_dtype, ldy, rows, cols, s);
-  return ln_dispatch<8>(x, x_dtype, ldx, resid, ldr, sum_out, lds, gamma, beta,
-                        eps, y, y_dtype, ldy, rows, cols, s);
+  // chunks of 8 per lane: 64 lanes x 8 = 512 columns per chunk
+  switch ((cols + 511) / 512) {
+#define WX_LNC(N)                                                                   \
+    case N:                                                                         \
+      return ln_dispatch<N>(x, x_dtype, ldx, resid, ldr, sum_out, lds, gamma, beta, \
+                            eps, y, y_dtype, ldy, rows, cols, stream, s);
+    WX_LNC(1) WX_LNC(2) WX_LNC(3) WX_LNC(4) WX_LNC(5) WX_LNC(6) WX_LNC(7) WX_LNC(8)
+#undef WX_LNC
+  }
+  return hipErrorInvalidValue;
 }
 
 // ======================================================== GELU
-__device__ __forceinline__ uint16_t gelu_variant(float x, int variant) {
-  if (variant == GELU_ERF) return f2bf(gelu_erf(x));
-  if (variant == GELU_POLY4_RNE) return f2bf(poly4_gelu_pre<true>(rb_rne(x)));
-  return f2bf_trunc(poly4_gelu_pre<false>(x));
+// The standalone GELU streams: every element is read once and written once,
+// so the loads and stores carry the non-temporal hint (the data is not
+// wanted in L2 or the Infinity Cache afterwards; on this GPU that lifts a
+// plain copy of the [1500, 5120] bf16 rowops shape from 3.9 to 5.2 TB/s).
+// A thread handles kGeluChunks 16-byte chunks per trip, loads first, then
+// math and stores.
+//
+// poly4 GELU with RNE (g4r, and g4f after its input rounding) by table: for
+// a bf16 input, the bump q of poly4_q depends only on the bit pattern of
+// |x|. At or below 2^-10 (pattern 0x3A80), rb(|x| - 0.5) is -0.5 (the tie
+// at 2^-10 goes to the even -0.5), so q equals q(0); from 4.0 (0x4080) up,
+// and for inf and NaN, q is 0. g_poly4_q holds q for the patterns
+// 0x3A80 .. 0x4080, written once per device by poly4_table_kernel from
+// poly4_q itself, so the table path returns the arithmetic path's bits; a
+// GELU workgroup copies it (3 KB) to LDS and looks q up by the pattern
+// clamped into that range: 9 operations and one LDS read per element in
+// place of ~35. The truncating variant (g4) keeps the arithmetic: under
+// truncation q is not constant below 2^-9.
+constexpr int kP4LutBase = 0x3A80;
+constexpr int kP4LutLen = 0x4080 - kP4LutBase + 1;      // 1537
+constexpr int kP4LutPad = (kP4LutLen + 7) / 8 * 8;      // 16-byte multiple
+__device__ __align__(16) uint16_t g_poly4_q[kP4LutPad];
+
+__global__ __launch_bounds__(256) void poly4_table_kernel() {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < kP4LutPad)
+    g_poly4_q[i] = i < kP4LutLen ? f2bf(poly4_q<true>(bf2f((uint16_t)(kP4LutBase + i)))) : 0;
 }
 
-template <int VARIANT, bool XF32>
+hipError_t init_rowop_tables(hipStream_t s) {
+  poly4_table_kernel<<<(kP4LutPad + 255) / 256, 256, 0, s>>>();
+  return hipGetLastError();
+}
+
+// poly4 GELU (RNE) of a bf16-exact x, q looked up in the LDS copy of the
+// table: the pattern of |x| clamped into [0x3A80, 0x4080] (v_med3_i32)
+__device__ __forceinline__ float poly4_gelu_lut(float x, const uint16_t* lut) {
+  const int bits = (int)(__float_as_uint(x) >> 16) & 0x7FFF;
+  const int idx = min(max(bits - kP4LutBase, 0), kP4LutLen - 1);
+  return fmaxf(x, 0.f) + bf2f(lut[idx]);
+}
+
+template <int VARIANT>
+__device__ __forceinline__ uint32_t gelu_pair(float a, float b, const uint16_t* lut) {
+  if (VARIANT == GELU_ERF) return f2bf2(gelu_erf(a), gelu_erf(b));
+  if (VARIANT == GELU_POLY4_RNE)
+    return f2bf2(poly4_gelu_lut(rb_rne(a), lut), poly4_gelu_lut(rb_rne(b), lut));
+  return (uint32_t)f2bf_trunc(poly4_gelu_pre<false>(a)) |
+         ((uint32_t)f2bf_trunc(poly4_gelu_pre<false>(b)) << 16);
+}
+
+// 16-byte chunks per thread per trip, and workgroups at most: the whole
+// grid for erf (one trip each), 1024 for the table variant, whose
+// workgroups each copy the 3 KB table first (measured on [1500, 5120]).
+constexpr int kGeluChunks = 2;
+constexpr int kGeluGridErf = 1 << 20, kGeluGridLut = 1024;
+
+// 8-element chunks i in [0, total8): chunk i is row i / cols8, columns
+// 8 (i % cols8) .. + 7 (CONTIG: the rows are packed, offset 8 i). The host
+// keeps total8 + the grid's stride below 2^32.
+template <int VARIANT, bool XF32, bool CONTIG, int CH>
 __global__ __launch_bounds__(256) void gelu_kernel_v8(
     const void* __restrict__ xp, int64_t ldx, uint16_t* __restrict__ y,
-    int64_t ldy, int rows, int cols8) {
-  const int64_t total = (int64_t)rows * cols8;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * 256) {
-    const int r = (int)(i / cols8);
-    const int64_t c = (i - (int64_t)r * cols8) * 8;
-    float v[8];
-    if (XF32) {
-      const float* x = static_cast<const float*>(xp) + r * ldx + c;
-      f32x4 a = *reinterpret_cast<const f32x4*>(x);
-      f32x4 b = *reinterpret_cast<const f32x4*>(x + 4);
+    int64_t ldy, uint32_t cols8, uint32_t total8) {
+  constexpr bool kLut = VARIANT == GELU_POLY4_RNE;
+  __shared__ __align__(16) uint16_t lut[kLut ? kP4LutPad : 8];
+  if (kLut) {
+    for (int i = threadIdx.x; i < kP4LutPad / 8; i += 256)
+      reinterpret_cast<u32x4*>(lut)[i] = reinterpret_cast<const u32x4*>(g_poly4_q)[i];
+    __syncthreads();
+  }
+  const uint32_t stride = gridDim.x * (256u * CH);
+  for (uint32_t base = blockIdx.x * (256u * CH) + threadIdx.x; base < total8;
+       base += stride) {
+    float v[CH][8];
+    int64_t oy[CH];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[j + 4] = b[j]; }
-    } else {
-      u16x8 a = *reinterpret_cast<const u16x8*>(
-          static_cast<const uint16_t*>(xp) + r * ldx + c);
+    for (int j = 0; j < CH; ++j) {
+      const uint32_t i = base + j * 256u;
+      if (i >= total8) continue;
+      int64_t ox;
+      if (CONTIG) {
+        ox = oy[j] = (int64_t)i * 8;
+      } else {
+        const uint32_t r = i / cols8, c = (i - r * cols8) * 8;
+        ox = r * ldx + c;
+        oy[j] = r * ldy + c;
+      }
+      if (XF32) {
+        const f32x4* x = reinterpret_cast<const f32x4*>(static_cast<const float*>(xp) + ox);
+        const f32x4 a = __builtin_nontemporal_load(x), b = __builtin_nontemporal_load(x + 1);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = bf2f(a[j]);
+        for (int k = 0; k < 4; ++k) { v[j][k] = a[k]; v[j][k + 4] = b[k]; }
+      } else {
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            static_cast<const uint16_t*>(xp) + ox));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[j][2 * k] = __uint_as_float(w[k] << 16);
+          v[j][2 * k + 1] = __uint_as_float(w[k] & 0xFFFF0000u);
+        }
+      }
     }
-    u16x8 o;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = gelu_variant(v[j], VARIANT);
-    *reinterpret_cast<u16x8*>(y + r * ldy + c) = o;
+    for (int j = 0; j < CH; ++j) {
+      if (base + j * 256u >= total8) continue;
+      u32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = gelu_pair<VARIANT>(v[j][2 * k], v[j][2 * k + 1], lut);
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(y + oy[j]));
+    }
   }
 }
 
+__device__ __forceinline__ uint16_t gelu_variant(float x, int variant, const uint16_t* lut) {
+  if (variant == GELU_ERF) return f2bf(gelu_erf(x));
+  if (variant == GELU_POLY4_RNE) return f2bf(poly4_gelu_lut(rb_rne(x), lut));
+  return f2bf_trunc(poly4_gelu_pre<false>(x));
+}
+
+// Any alignment and width, one element per thread and trip.
 template <int VARIANT, bool XF32>
 __global__ __launch_bounds__(256) void gelu_kernel_scalar(
     const void* __restrict__ xp, int64_t ldx, uint16_t* __restrict__ y,
     int64_t ldy, int rows, int cols) {
+  constexpr bool kLut = VARIANT == GELU_POLY4_RNE;
+  __shared__ __align__(16) uint16_t lut[kLut ? kP4LutPad : 8];
+  if (kLut) {
+    for (int i = threadIdx.x; i < kP4LutPad / 8; i += 256)
+      reinterpret_cast<u32x4*>(lut)[i] = reinterpret_cast<const u32x4*>(g_poly4_q)[i];
+    __syncthreads();
+  }
   const int64_t total = (int64_t)rows * cols;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
@@ -219,7 +409,7 @@ __global__ __launch_bounds__(256) void gelu_kernel_scalar(
     const int64_t c = i - (int64_t)r * cols;
     const float v = XF32 ? static_cast<const float*>(xp)[r * ldx + c]
                          : bf2f(static_cast<const uint16_t*>(xp)[r * ldx + c]);
-    y[r * ldy + c] = gelu_variant(v, VARIANT);
+    y[r * ldy + c] = gelu_variant(v, VARIANT, lut);
   }
 }
 
@@ -235,21 +425,34 @@ static hipError_t gelu_dispatch(const void* x, bool xf, int64_t ldx,
                                 hipStream_t s) {
   const size_t xe = xf ? 4 : 2;
   const bool vec = (cols % 8 == 0) && (ldx % 8 == 0) && (ldy % 8 == 0) &&
-                   ((uintptr_t)x % (xe * 8 > 16 ? 16 : xe * 8) == 0) &&
-                   ((uintptr_t)y % 16 == 0);
-  if (vec) {
-    const int cols8 = cols / 8;
-    const int g = grid_for((int64_t)rows * cols8);
-    if (xf)
-      gelu_kernel_v8<VARIANT, true><<<g, 256, 0, s>>>(x, ldx, y, ldy, rows, cols8);
-    else
-      gelu_kernel_v8<VARIANT, false><<<g, 256, 0, s>>>(x, ldx, y, ldy, rows, cols8);
-  } else {
+                   ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+  if (!vec) {
     const int g = grid_for((int64_t)rows * cols);
     if (xf)
       gelu_kernel_scalar<VARIANT, true><<<g, 256, 0, s>>>(x, ldx, y, ldy, rows, cols);
     else
       gelu_kernel_scalar<VARIANT, false><<<g, 256, 0, s>>>(x, ldx, y, ldy, rows, cols);
+    return hipGetLastError();
+  }
+  const uint32_t cols8 = (uint32_t)(cols / 8);
+  const bool contig = ldx == cols && ldy == cols;
+  // row bands of at most 2^30 chunks keep every 32-bit chunk index (plus
+  // the grid's stride) below 2^32
+  const int band = (int)std::min<int64_t>(rows, (int64_t)(1u << 30) / cols8);
+  for (int r0 = 0; r0 < rows; r0 += band) {
+    const int nr = std::min(band, rows - r0);
+    const uint32_t total8 = (uint32_t)nr * cols8;
+    constexpr int cap = VARIANT == GELU_POLY4_RNE ? kGeluGridLut : kGeluGridErf;
+    const int g = (int)std::min<int64_t>((total8 + 256 * kGeluChunks - 1) / (256 * kGeluChunks),
+                                         cap);
+    const void* xb = static_cast<const char*>(x) + (int64_t)r0 * ldx * xe;
+    uint16_t* yb = y + (int64_t)r0 * ldy;
+#define WX_GELU(XF, CG)                                                     \
+    if (xf == XF && contig == CG)                                           \
+      gelu_kernel_v8<VARIANT, XF, CG, kGeluChunks><<<g, 256, 0, s>>>(xb, ldx, yb, ldy, cols8, \
+                                                                    total8);
+    WX_GELU(true, true) WX_GELU(true, false) WX_GELU(false, true) WX_GELU(false, false)
+#undef WX_GELU
   }
   return hipGetLastError();
 }
@@ -271,6 +474,9 @@ hipError_t launch_gelu(const void* x, int x_dtype, int64_t ldx, uint16_t* y,
 }
 
 // ======================================================== softmax
+// Rows are read once and written once: loads and stores carry the
+// non-temporal hint (buffer loads: cache-policy bit 1, NT on this GPU).
+constexpr int kCpolNt = 2;
 // One wave per row, VEC-element chunks held in registers (MAXCH per lane).
 template <int VEC, int MAXCH>
 __global__ __launch_bounds__(256) void softmax_kernel(
@@ -288,11 +494,11 @@ __global__ __launch_bounds__(256) void softmax_kernel(
     const int ch = lane + c * 64;
     if (ch < nch) {
       if (VEC == 8) {
-        u16x8 a = *reinterpret_cast<const u16x8*>(xr + ch * 8);
+        u16x8 a = __builtin_nontemporal_load(reinterpret_cast<const u16x8*>(xr + ch * 8));
 #pragma unroll
         for (int j = 0; j < VEC; ++j) v[c][j] = bf2f(a[j]);
       } else if (VEC == 4) {
-        u16x4 a = *reinterpret_cast<const u16x4*>(xr + ch * 4);
+        u16x4 a = __builtin_nontemporal_load(reinterpret_cast<const u16x4*>(xr + ch * 4));
 #pragma unroll
         for (int j = 0; j < VEC; ++j) v[c][j] = bf2f(a[j]);
       } else {
@@ -327,11 +533,11 @@ __global__ __launch_bounds__(256) void softmax_kernel(
       u32x4 pk;
 #pragma unroll
       for (int j = 0; j < 4; ++j) pk[j] = f2bf2(v[c][2 * j] * inv, v[c][2 * j + 1] * inv);
-      *reinterpret_cast<u32x4*>(yr + ch * 8) = pk;
+      __builtin_nontemporal_store(pk, reinterpret_cast<u32x4*>(yr + ch * 8));
     } else if (VEC == 4) {
       u32x2 pk = {f2bf2(v[c][0] * inv, v[c][1] * inv),
                   f2bf2(v[c][2] * inv, v[c][3] * inv)};
-      *reinterpret_cast<u32x2*>(yr + ch * 4) = pk;
+      __builtin_nontemporal_store(pk, reinterpret_cast<u32x2*>(yr + ch * 4));
     } else {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) yr[ch * VEC + j] = f2bf(v[c][j] * inv);
@@ -351,18 +557,55 @@ __global__ __launch_bounds__(256) void softmax_kernel(
 // exp is one FMA and one exp2 per element: p = 2^(x log2e - m log2e + 32)
 // / sum; the +32 keeps exp2's result out of the denormal range for every p
 // that is representable, and cancels in the division.
+// One row's MAXCH chunk slots per lane, loaded unconditionally: a slot past
+// the row's last chunk gets an offset beyond the descriptor's range, so it
+// reads zeros without touching memory (the row math masks it). Not for the
+// last row, whose last chunk may cross the end of the input.
+constexpr uint32_t kOutOfRange = 0x80000000u;  // > any x_bytes (< 2^31)
 template <int MAXCH>
-__global__ __launch_bounds__(256) void softmax_kernel_span(
-    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y,
-    int64_t ldy, int rows, int valid, int x_bytes) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, x_bytes, 0x00020000);
-  const int64_t sx = (int64_t)row * ldx, sy = (int64_t)row * ldy;
+__device__ __forceinline__ void softmax_span_load(u32x4 (&w)[MAXCH], __amdgpu_buffer_rsrc_t rx,
+                                                  int64_t sx, int lane, int nch) {
+  const uint32_t a = (uint32_t)((sx & ~(int64_t)7) * 2);
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) {
+    const int c = lane + i * 64;
+    const uint32_t off = c < nch ? a + (uint32_t)c * 16 : kOutOfRange;
+    w[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, kCpolNt);
+  }
+}
+
+// The last row: the chunk that can run past the end of the input is read
+// element by element (a 16-byte access that crosses the descriptor's range
+// reads as all zeros).
+template <int MAXCH>
+__device__ __forceinline__ void softmax_span_load_last(u32x4 (&w)[MAXCH], __amdgpu_buffer_rsrc_t rx,
+                                                       const uint16_t* __restrict__ x, int64_t sx,
+                                                       int lane, int valid) {
   const int head = (int)(sx & 7);
-  const int64_t ax = sx - head, ay = sy - head;  // ldx == ldy (mod 8): same head
+  const int nch = (head + valid + 7) >> 3;
+  softmax_span_load<MAXCH>(w, rx, sx, lane, nch);
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) {
+    const int c = lane + i * 64;
+    if (c != nch - 1) continue;
+    uint32_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = c * 8 + j - head;
+      e[j] = (k >= 0 && k < valid) ? x[sx + k] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[i][j] = e[2 * j] | (e[2 * j + 1] << 16);
+  }
+}
+
+// softmax of one row from its loaded chunks; stores to y
+template <int MAXCH>
+__device__ __forceinline__ void softmax_span_row(const u32x4 (&w)[MAXCH], uint16_t* __restrict__ y,
+                                                 int64_t sx, int64_t sy, int lane, int valid) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  const int head = (int)(sx & 7);
+  const int64_t ay = sy - head;  // ldx == ldy (mod 8): same head
   const int nch = (head + valid + 7) >> 3;
   float v[MAXCH][8];
   float m = -INFINITY;
@@ -370,48 +613,30 @@ __global__ __launch_bounds__(256) void softmax_kernel_span(
   for (int i = 0; i < MAXCH; ++i) {
     const int c = lane + i * 64;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[i][j] = -INFINITY;
-    if (c < nch) {
-      if (row == rows - 1 && c == nch - 1) {
-        // the one chunk that may run past the end of the input: a 16-byte
-        // access that crosses the descriptor's range reads as all zeros, so
-        // its in-row elements are read one by one
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int e = c * 8 + j - head;
-          if (e >= 0 && e < valid) v[i][j] = bf2f(x[sx + e]);
-        }
-      } else {
-        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)((ax + c * 8) * 2), 0, 0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[i][2 * j] = __uint_as_float(w[j] << 16);
-          v[i][2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-        }
-      }
-      if (c == 0 || c == nch - 1) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int e = c * 8 + j - head;
-          if (e < 0 || e >= valid) v[i][j] = -INFINITY;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) m = fmaxf(m, v[i][j]);
+    for (int j = 0; j < 4; ++j) {
+      v[i][2 * j] = __uint_as_float(w[i][j] << 16);
+      v[i][2 * j + 1] = __uint_as_float(w[i][j] & 0xFFFF0000u);
     }
+    if (c == 0 || c >= nch - 1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = c * 8 + j - head;
+        if (e < 0 || e >= valid) v[i][j] = -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, v[i][j]);
   }
   m = wave_max(m);
-  constexpr float kLog2e = 1.4426950408889634f;
   const float off = 32.0f - m * kLog2e;
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXCH; ++i) {
-    if (lane + i * 64 < nch) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        v[i][j] = __builtin_amdgcn_exp2f(fmaf(v[i][j], kLog2e, off));
-        sum += v[i][j];
-      }
+    for (int j = 0; j < 8; ++j) {
+      // masked elements give exp2(-inf) = 0
+      v[i][j] = __builtin_amdgcn_exp2f(fmaf(v[i][j], kLog2e, off));
+      sum += v[i][j];
     }
   }
   const float inv = 1.0f / wave_sum(sum);
@@ -429,9 +654,27 @@ __global__ __launch_bounds__(256) void softmax_kernel_span(
       u32x4 pk;
 #pragma unroll
       for (int j = 0; j < 4; ++j) pk[j] = f2bf2(v[i][2 * j] * inv, v[i][2 * j + 1] * inv);
-      *reinterpret_cast<u32x4*>(y + ay + c * 8) = pk;
+      __builtin_nontemporal_store(pk, reinterpret_cast<u32x4*>(y + ay + c * 8));
     }
   }
+}
+
+template <int MAXCH>
+__global__ __launch_bounds__(256) void softmax_kernel_span(
+    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y,
+    int64_t ldy, int rows, int valid, int x_bytes) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const int lane = threadIdx.x & 63;
+  const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (row >= rows) return;
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, x_bytes, 0x00020000);
+  u32x4 w[MAXCH];
+  const int64_t sx = (int64_t)row * ldx;
+  if (row < rows - 1)
+    softmax_span_load<MAXCH>(w, rx, sx, lane, ((int)(sx & 7) + valid + 7) >> 3);
+  else
+    softmax_span_load_last<MAXCH>(w, rx, x, (int64_t)row * ldx, lane, valid);
+  softmax_span_row<MAXCH>(w, y, (int64_t)row * ldx, (int64_t)row * ldy, lane, valid);
 #endif
 }
 
