@@ -16,6 +16,10 @@ KERNEL is one of
   qkv        A [B*1500, 1280] . Wqkv [3840, 1280]^T split into Q, K, Vt
   out_proj   A [B*1500, 1280] . Wo [1280, 1280]^T + bo into the fp32 residual
   attention  softmax(Q K^T / 8) V over B*20 heads of 1500 keys
+  rowops     the row kernels on the standalone rowops shapes, N launches each
+             on one buffer pair per kernel: LayerNorm [1500, 1280] bf16 and
+             [24000, 1280] fp32 -> bf16, erf-GELU and poly4-GELU (g4r)
+             [1500, 5120] bf16, softmax [30000, 1500] bf16
 """
 import argparse
 import sys
@@ -29,7 +33,7 @@ COPY_BYTES = 512 << 20
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("kernel", choices=["fc1", "fc2", "qkv", "out_proj", "attention"])
+    ap.add_argument("kernel", choices=["fc1", "fc2", "qkv", "out_proj", "attention", "rowops"])
     ap.add_argument("--reps", type=int, default=4)
     ap.add_argument("--batch", type=int, default=16)
     args = ap.parse_args()
@@ -62,6 +66,33 @@ def main():
         else:
             x = normal((M, N), 1.0, torch.float32)
             run = lambda: dev.gemm(A, W, b, L.WXH_EPI_RESID_F32, out=x)
+    elif args.kernel == "rowops":
+        def rowop_runs():
+            cases = []
+            x = normal((1500, 1280), 2.0)
+            gm = 1 + normal((1280,), 0.1, torch.float32)
+            bt = normal((1280,), 0.1, torch.float32)
+            y = torch.empty_like(x)
+            cases.append(("layernorm 1500x1280 bf16", lambda: dev.layer_norm(x, gm, bt, out=y)))
+            xf = normal((24000, 1280), 2.0, torch.float32)
+            yf = torch.empty(24000, 1280, dtype=torch.bfloat16, device=dev.device)
+            cases.append(("layernorm 24000x1280 f32->bf16",
+                          lambda: dev.layer_norm(xf, gm, bt, out=yf)))
+            xg = normal((1500, 5120), 3.0)
+            yg = torch.empty_like(xg)
+            cases.append(("gelu erf 1500x5120", lambda: dev.gelu(xg, L.WXH_GELU_ERF, out=yg)))
+            cases.append(("gelu poly4 1500x5120",
+                          lambda: dev.gelu(xg, L.WXH_GELU_POLY4_RNE, out=yg)))
+            xs = normal((30000, 1500), 4.0)
+            ys = torch.empty_like(xs)
+            cases.append(("softmax 30000x1500", lambda: dev.softmax_rows(xs, out=ys)))
+            return cases
+
+        cases = rowop_runs()
+
+        def run():
+            for name, fn in cases:
+                fn()
     else:
         Q, Kt, Vt = dev.attn_buffers(args.batch, NH, CTX)
         for t in (Q, Kt, Vt):
@@ -75,7 +106,8 @@ def main():
     for i in range(args.reps):
         run()
     dev.synchronize()
-    print(f"[probe] {args.kernel} batch {args.batch} x {args.reps}", flush=True)
+    what = "rowops shapes" if args.kernel == "rowops" else f"batch {args.batch}"
+    print(f"[probe] {args.kernel} {what} x {args.reps}", flush=True)
 
 
 if __name__ == "__main__":
