@@ -39,7 +39,7 @@ enum {
   WXH_ERR_STATE = 5        /* e.g. encoder weights incomplete */
 };
 
-enum { WXH_BF16 = 0, WXH_F32 = 1 };
+enum { WXH_BF16 = 0, WXH_F32 = 1, WXH_I8 = 2 };
 
 /* GELU variants. ERF: exact erf-GELU (npu_whisper_encoder.py:284-287).
  * POLY4_RNE: poly4 with round-to-nearest-even (rowop codes g4r, and g4f when
@@ -53,7 +53,8 @@ enum {
   WXH_EPI_BF16 = 1,            /* C bf16 = A.W^T + bias                      */
   WXH_EPI_BF16_GELU_ERF = 2,   /* C bf16 = gelu_erf(A.W^T + bias)            */
   WXH_EPI_BF16_GELU_POLY4 = 3, /* C bf16 = poly4 g4f (A.W^T + bias)          */
-  WXH_EPI_RESID_F32 = 4        /* C fp32 += A.W^T + bias (residual add)      */
+  WXH_EPI_RESID_F32 = 4,       /* C fp32 += A.W^T + bias (residual add)      */
+  WXH_EPI_F32_GELU_ERF = 5     /* C fp32 = gelu_erf(A.W^T + bias) (int8 GEMM) */
 };
 
 /* Fault-injection bits: a masked entry point returns WXH_ERR_INJECTED before
@@ -175,6 +176,35 @@ int wxh_gemm_bf16(wxh_ctx* ctx, int M, int N, int K, const uint16_t* A,
                   const float* bias, void* C, int64_t ldc, int epilogue,
                   void* stream);
 
+/* ------------------------------------------------------------------ int8 */
+
+/* Symmetric int8 quantisation of a rows x cols band of x (WXH_F32 or
+ * WXH_BF16), the reference's quantised matmul's rule
+ * (bench/probe_int8_decode.py:58-66): scale = max|x| / 127 (1 when all
+ * zero), q = rint(x / scale) (round half to even) as int8, fp32 arithmetic.
+ * per_tensor = 0: one scale per row, scale[rows] (per-token activations;
+ * for a weight in (out, in) layout, per output channel, the reference's
+ * "perchan" mode). per_tensor = 1: one scale for the band in scale[0]
+ * (its "pertensor" mode). q rows hold cols_pad >= cols codes, the columns
+ * past cols zero. cols % 8 == 0, ldx % 8 == 0, ldq % 8 == 0, cols_pad % 8
+ * == 0, cols_pad <= 8192, x 16-byte and q 8-byte aligned. */
+int wxh_quantize_rows(wxh_ctx* ctx, const void* x, int x_dtype, int64_t ldx,
+                      int rows, int cols, int8_t* q, int64_t ldq, int cols_pad,
+                      float* scale, int per_tensor, void* stream);
+
+/* C[M,N] = ((float)(A_q . W_q^T)[m,n] * a_scale[m]) * w_scale[n] (+ bias[n])
+ * with an epilogue (WXH_EPI_F32, _BF16, _BF16_GELU_ERF, _RESID_F32,
+ * _F32_GELU_ERF). A_q int8 [M, K] (lda), W_q int8 [N, K] (ldw, torch's
+ * (out, in) layout); the int32 dot products are exact and rounded once to
+ * fp32, in the reference's order (bench/probe_int8_decode.py:67-71).
+ * K % 128 == 0 (zero-pad K), lda % 16 == 0, ldw % 16 == 0, A and W 16-byte
+ * aligned. Replaces the reference's q_matmul plug (probe_int8_decode.py:48-74)
+ * for the projection, MLP and conv GEMMs. */
+int wxh_gemm_i8(wxh_ctx* ctx, int M, int N, int K, const int8_t* A, int64_t lda,
+                const float* a_scale, const int8_t* W, int64_t ldw,
+                const float* w_scale, const float* bias, void* C, int64_t ldc,
+                int epilogue, void* stream);
+
 /* ------------------------------------------------------------------ attention */
 
 /* Padded key length Tp used by the attention operand layouts (T rounded up
@@ -250,6 +280,21 @@ int wxh_encoder_forward_host(wxh_encoder* enc, const float* mel_host,
 
 /* Enable (default) or disable hipGraph capture/replay of the forward body. */
 int wxh_encoder_set_graph(wxh_encoder* enc, int enabled);
+
+/* Keep int8 copies of the GEMM weights (per output channel scales, from the
+ * fp32 values) as they are set; must be called before the first
+ * wxh_encoder_set_weight. Needs d_model % 128 == 0 and the erf MLP GELU. */
+int wxh_encoder_enable_int8(wxh_encoder* enc);
+
+/* Run the forward with int8 GEMMs (on = 1) or bf16 (0, the default): every
+ * conv, projection and MLP GEMM quantises its A operand per token and its
+ * weight per output channel, as encoder(W, mel, q_matmul_factory("perchan"),
+ * np_matmul, fold_bias=False) does in the reference
+ * (bench/probe_int8_decode.py:48-74, 143-145); attention stays bf16 MFMA.
+ * The A operands are quantised from fp32 values: the fp32 LayerNorm output
+ * (in the LayerNorm kernel), the fp32 attention output, the fp32 GELU of
+ * fc1, and the conv im2col rows of the fp32 mel and conv1 output. */
+int wxh_encoder_set_int8(wxh_encoder* enc, int on);
 
 /* Per-stage device time of one un-graphed forward, measured with HIP events
  * on the stream the kernels run on. ms[i] (i < n) receives the summed time

@@ -11,6 +11,8 @@ bf16      fp32 <-> bf16 bit conversions (round-to-nearest-even and truncation)
 rowops    the row-wise definitions: LayerNorm, erf-GELU, poly4-GELU, softmax
 encoder   the encoder restated twice: torch fp32 (nn ops) and numpy (im2col)
 audio     whisper's log-mel front end (numpy float64 STFT, Slaney filterbank)
+int8      the reference's int8 quantised matmul (per-token / per-channel or
+          per-tensor scales) and the encoder run with it
 poly4.c   an independent C restatement of the poly4 GELU, built by ``build.py``
 
 Every function cites the reference file:line it restates. How each function

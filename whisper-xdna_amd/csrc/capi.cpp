@@ -14,6 +14,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 #include <map>
@@ -67,6 +68,7 @@ struct wxh_ctx {
   std::map<int, uint8_t*> logmel;  // n_mels -> device constants (log-mel front end)
   int* logmel_slots = nullptr;     // per-clip maxima scratch of wxh_log_mel
   int logmel_cap = 0;              // clips it holds
+  unsigned* absmax_bits = nullptr; // per-tensor scale scratch of wxh_quantize_rows
 };
 
 namespace {
@@ -131,6 +133,7 @@ void ctx_release(wxh_ctx* c) {
   (void)hipStreamDestroy(c->stream);
   for (auto& kv : c->logmel) (void)hipFree(kv.second);
   if (c->logmel_slots) (void)hipFree(c->logmel_slots);
+  if (c->absmax_bits) (void)hipFree(c->absmax_bits);
   delete c;
 }
 }  // namespace
@@ -300,6 +303,67 @@ int wxh_gemm_bf16(wxh_ctx* c, int M, int N, int K, const uint16_t* A,
   return WXH_OK;
 }
 
+// ------------------------------------------------------------------ int8
+
+int wxh_quantize_rows(wxh_ctx* c, const void* x, int x_dtype, int64_t ldx, int rows,
+                      int cols, int8_t* q, int64_t ldq, int cols_pad, float* scale,
+                      int per_tensor, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_GEMM, "wxh_quantize_rows")) return r;
+  WXH_REQUIRE(x && q && scale, "wxh_quantize_rows: null pointer");
+  WXH_REQUIRE(x_dtype == WXH_F32 || x_dtype == WXH_BF16, "wxh_quantize_rows: x_dtype");
+  WXH_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && ldx >= cols && ldx % 8 == 0,
+              "wxh_quantize_rows: cols=%d ldx=%lld must be multiples of 8 (ldx >= cols)",
+              cols, (long long)ldx);
+  WXH_REQUIRE(cols_pad >= cols && cols_pad % 8 == 0 && cols_pad <= 8192 && ldq >= cols_pad &&
+                  ldq % 8 == 0,
+              "wxh_quantize_rows: cols_pad=%d ldq=%lld (multiples of 8, cols <= cols_pad <= "
+              "8192, ldq >= cols_pad)",
+              cols_pad, (long long)ldq);
+  WXH_REQUIRE(aligned16(x) && ((uintptr_t)q & 7) == 0,
+              "wxh_quantize_rows: x must be 16-byte and q 8-byte aligned");
+  hipStream_t s = pick(c, stream);
+  if (per_tensor) {
+    if (!c->absmax_bits) WXH_HIP(hipMalloc(&c->absmax_bits, 256));
+    WXH_HIP(wx::launch_absmax_scale(x, x_dtype, ldx, rows, cols, scale, c->absmax_bits, s));
+  }
+  WXH_HIP(wx::launch_quantize_rows(x, x_dtype, ldx, rows, cols, q, ldq, cols_pad, scale,
+                                   per_tensor != 0, s));
+  return WXH_OK;
+}
+
+int wxh_gemm_i8(wxh_ctx* c, int M, int N, int K, const int8_t* A, int64_t lda,
+                const float* a_scale, const int8_t* W, int64_t ldw, const float* w_scale,
+                const float* bias, void* C, int64_t ldc, int epilogue, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_GEMM, "wxh_gemm_i8")) return r;
+  WXH_REQUIRE(A && W && C && a_scale && w_scale, "wxh_gemm_i8: null operand or scale");
+  WXH_REQUIRE(M >= 0 && N >= 0 && K > 0, "wxh_gemm_i8: bad size");
+  WXH_REQUIRE(K % wx::kI8KAlign == 0 && lda % 16 == 0 && ldw % 16 == 0 && lda >= K &&
+                  ldw >= K,
+              "wxh_gemm_i8: K=%d must be a multiple of %d (zero-pad), lda=%lld ldw=%lld "
+              "multiples of 16 (>= K)",
+              K, wx::kI8KAlign, (long long)lda, (long long)ldw);
+  WXH_REQUIRE(ldc >= N, "wxh_gemm_i8: ldc < N");
+  WXH_REQUIRE(aligned16(A) && aligned16(W), "wxh_gemm_i8: A/W must be 16-byte aligned");
+  wx::EpiParams e;
+  e.out = C;
+  e.ldo = ldc;
+  e.bias = bias;
+  e.a_scale = a_scale;
+  e.w_scale = w_scale;
+  int mode;
+  switch (epilogue) {
+    case WXH_EPI_F32: mode = wx::EPI_F32; break;
+    case WXH_EPI_BF16: mode = wx::EPI_BF16; break;
+    case WXH_EPI_BF16_GELU_ERF: mode = wx::EPI_BF16; e.gelu = wx::GELU_ERF; break;
+    case WXH_EPI_RESID_F32: mode = wx::EPI_RESID; break;
+    case WXH_EPI_F32_GELU_ERF: mode = wx::EPI_F32_GELU; break;
+    default: return fail(WXH_ERR_INVALID, "wxh_gemm_i8: unsupported epilogue %d", epilogue);
+  }
+  wx::GemmA a{A, lda, M > 0 ? M : 1, 0};
+  WXH_HIP(wx::launch_gemm_i8(M, N, K, a, W, ldw, mode, e, pick(c, stream)));
+  return WXH_OK;
+}
+
 // ------------------------------------------------------------------ attention
 
 int wxh_attention_padded_len(int T) { return wx::attn_padded_len(T); }
@@ -356,6 +420,15 @@ struct LayerW {
   float* ln1_b = nullptr;
   float* ln2_g = nullptr;
   float* ln2_b = nullptr;
+  // int8 copies (wxh_encoder_enable_int8): codes and per-output-channel scales
+  int8_t* wqkv_q = nullptr;
+  int8_t* wo_q = nullptr;
+  int8_t* w1_q = nullptr;
+  int8_t* w2_q = nullptr;
+  float* sqkv = nullptr;
+  float* so = nullptr;
+  float* s1 = nullptr;
+  float* s2 = nullptr;
 };
 
 enum Stage {
@@ -398,6 +471,18 @@ struct wxh_encoder {
   std::vector<void*> ws_allocs;
   bool use_graph = true;
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+  // int8 GEMM path
+  bool i8_weights = false;   // int8 weight copies are kept (enable_int8)
+  bool i8 = false;           // the forward runs the int8 path (set_int8)
+  int k1p = 0;               // conv1 K (3 n_mels) padded to a multiple of 128
+  int8_t* conv1_q = nullptr; // [d, k1p], K index j*n_mels + c
+  int8_t* conv2_q = nullptr; // [d, 3d]
+  float* conv1_s = nullptr;
+  float* conv2_s = nullptr;
+  int64_t cap_aq = 0, cap_asc = 0, cap_f32 = 0;
+  int8_t* aq = nullptr;      // quantised A operand of the current GEMM
+  float* asc = nullptr;      // its per-row scales
+  float* f32ws = nullptr;    // fp32 staging: mel^T, conv1 out, attention out, GELU(fc1)
 };
 
 namespace {
@@ -441,13 +526,19 @@ int ensure_stage(wxh_encoder* E, size_t n) {
   return WXH_OK;
 }
 
-// host fp32 [rows, cols] -> device bf16 via the conversion kernel (RNE)
-int upload_bf16(wxh_encoder* E, uint16_t* dst, const float* host, int rows, int cols) {
+// host fp32 [rows, cols] -> device bf16 via the conversion kernel (RNE);
+// with q, also int8 codes [rows, q_ld] and a scale per row (output
+// channel), quantised from the fp32 values
+int upload_bf16(wxh_encoder* E, uint16_t* dst, const float* host, int rows, int cols,
+                int8_t* q = nullptr, float* q_scale = nullptr, int q_ld = 0) {
   const size_t n = (size_t)rows * cols;
   if (int r = ensure_stage(E, n)) return r;
   hipStream_t s = E->ctx->stream;
   WXH_HIP(hipMemcpyAsync(E->stage, host, n * sizeof(float), hipMemcpyHostToDevice, s));
   WXH_HIP(wx::launch_convert(E->stage, cols, dst, cols, rows, cols, false, s));
+  if (q)
+    WXH_HIP(wx::launch_quantize_rows(E->stage, wx::DT_F32, cols, rows, cols, q, q_ld, q_ld,
+                                     q_scale, false, s));
   WXH_HIP(hipStreamSynchronize(s));
   return WXH_OK;
 }
@@ -494,12 +585,22 @@ int ensure_workspace(wxh_encoder* E, int batch, int frames) {
   const int64_t need_x = B * ctx * D.d_model;
   const int64_t need_qkv = B * D.n_head * tp * 64;
   const int64_t need_f = B * ctx * E->ffn;
+  // int8 path: the quantised A operand (conv1 im2col, conv2 im2col or
+  // [M, ffn]), its row scales, and fp32 staging
+  const int64_t d = D.d_model;
+  const int64_t need_aq =
+      E->i8 ? std::max({B * T * E->k1p, B * ctx * 3 * d, B * ctx * E->ffn}) : 0;
+  const int64_t need_asc = E->i8 ? B * T : 0;
+  const int64_t need_f32 =
+      E->i8 ? std::max({B * T * (int64_t)D.n_mels, B * T * d, B * ctx * E->ffn}) : 0;
   if (need_mel <= E->cap_mel && need_x1 <= E->cap_x1 && need_x <= E->cap_x &&
-      need_qkv <= E->cap_qkv && need_f <= E->cap_f)
+      need_qkv <= E->cap_qkv && need_f <= E->cap_f && need_aq <= E->cap_aq &&
+      need_asc <= E->cap_asc && need_f32 <= E->cap_f32)
     return WXH_OK;
   drop_graphs(E);
   free_list(E->ws_allocs);
   E->cap_mel = E->cap_x1 = E->cap_x = E->cap_qkv = E->cap_f = 0;
+  E->cap_aq = E->cap_asc = E->cap_f32 = 0;
   auto& L = E->ws_allocs;
   // pads (conv rows, attention key/query tails) must hold finite values:
   // everything starts zeroed, and later writes only ever store finite bf16
@@ -514,6 +615,14 @@ int ensure_workspace(wxh_encoder* E, int batch, int frames) {
   if (int r = dalloc(L, &E->f, need_f, true)) return r;
   if (int r = dalloc(L, &E->sk_ws, (size_t)kSplitKElems, false)) return r;
   if (int r = dalloc(L, &E->sk_cnt, (size_t)kSplitKTiles, true)) return r;
+  if (E->i8) {
+    if (int r = dalloc(L, &E->aq, (size_t)need_aq, true)) return r;
+    if (int r = dalloc(L, &E->asc, (size_t)need_asc, true)) return r;
+    if (int r = dalloc(L, &E->f32ws, (size_t)need_f32, true)) return r;
+    E->cap_aq = need_aq;
+    E->cap_asc = need_asc;
+    E->cap_f32 = need_f32;
+  }
   E->cap_mel = need_mel;
   E->cap_x1 = need_x1;
   E->cap_x = need_x;
@@ -549,7 +658,115 @@ struct StageTimer {
 
 // Launch the forward body (conv1 .. last layer). Stage events are recorded
 // after each launch when `timer` is set (un-graphed profiling only).
+// The int8 forward body. Every GEMM takes int8 A (quantised per row) and W
+// (per output channel) and runs launch_gemm_i8; the A operands come from
+// fp32 values: the conv im2col rows of the transposed fp32 mel (f32ws,
+// written before the graph) and of the fp32 conv1 output, the LayerNorm's
+// fp32 result (quantised in the LayerNorm kernel), the fp32 attention
+// output and the fp32 GELU(fc1).
+int run_body_i8(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* timer) {
+  const auto& D = E->dims;
+  const int d = D.d_model, nh = D.n_head, T = frames, C = D.n_mels;
+  const int ctx = (T - 1) / 2 + 1;
+  const int tp = wx::attn_padded_len(ctx);
+  const int M = batch * ctx, ffn = E->ffn;
+  auto mark = [&](int stage) -> int {
+    if (!timer) return WXH_OK;
+    hipEvent_t ev;
+    WXH_HIP(hipEventCreate(&ev));
+    WXH_HIP(hipEventRecord(ev, s));
+    timer->marks.push_back({stage, ev});
+    return WXH_OK;
+  };
+  auto gemm = [&](int m, int n, int k, const int8_t* w, const float* wsc, int mode,
+                  wx::EpiParams e) -> int {
+    e.a_scale = E->asc;
+    e.w_scale = wsc;
+    wx::GemmA a{E->aq, k, m, 0};
+    WXH_HIP(wx::launch_gemm_i8(m, n, k, a, w, k, mode, e, s));
+    return WXH_OK;
+  };
+  {  // conv1: im2col rows of mel^T (f32ws), GELU, fp32 out into f32ws
+    WXH_HIP(wx::launch_im2col_quant(E->f32ws, batch, T, C, 1, T, E->aq, E->k1p, E->asc, s));
+    wx::EpiParams e;
+    e.out = E->f32ws;
+    e.ldo = d;
+    e.bias = E->conv1_b;
+    if (int r = gemm(batch * T, d, E->k1p, E->conv1_q, E->conv1_s, wx::EPI_F32_GELU, e)) return r;
+    if (int r = mark(ST_CONV1)) return r;
+  }
+  {  // conv2: stride-2 im2col rows of the conv1 output, GELU, + positional embedding
+    WXH_HIP(wx::launch_im2col_quant(E->f32ws, batch, T, d, 2, ctx, E->aq, 3 * d, E->asc, s));
+    wx::EpiParams e;
+    e.out = E->x;
+    e.ldo = d;
+    e.bias = E->conv2_b;
+    e.aux = E->pos;
+    e.rows_per_batch = ctx;
+    if (int r = gemm(M, d, 3 * d, E->conv2_q, E->conv2_s, wx::EPI_CONV2, e)) return r;
+    if (int r = mark(ST_CONV2)) return r;
+  }
+  const float scale = 1.0f / 8.0f;  // (hd^-1/4)^2 with hd = 64
+  for (int l = 0; l < D.n_layer; ++l) {
+    const LayerW& W = E->layers[l];
+    WXH_HIP(wx::launch_layernorm(E->x, wx::DT_F32, d, nullptr, 0, nullptr, 0, W.ln1_g,
+                                 W.ln1_b, 1e-5f, E->aq, wx::DT_I8, d, M, d, false, s,
+                                 E->asc));
+    if (int r = mark(ST_LN)) return r;
+    {
+      wx::EpiParams e;
+      e.bias = W.bqkv;
+      e.q = E->q;
+      e.k = E->k;
+      e.vt = E->vt;
+      e.n_head = nh;
+      e.t_pad = tp;
+      e.d_model = d;
+      e.rows_per_batch = ctx;
+      if (int r = gemm(M, 3 * d, d, W.wqkv_q, W.sqkv, wx::EPI_QKV, e)) return r;
+      if (int r = mark(ST_QKV)) return r;
+    }
+    WXH_HIP(wx::launch_attention(E->q, E->k, E->vt, batch, nh, ctx, scale, E->f32ws,
+                                 wx::DT_F32, d, s));
+    if (int r = mark(ST_ATTN)) return r;
+    {
+      WXH_HIP(wx::launch_quantize_rows(E->f32ws, wx::DT_F32, d, M, d, E->aq, d, d, E->asc,
+                                       false, s));
+      wx::EpiParams e;
+      e.out = E->x;
+      e.ldo = d;
+      e.bias = W.bo;
+      if (int r = gemm(M, d, d, W.wo_q, W.so, wx::EPI_RESID, e)) return r;
+      if (int r = mark(ST_OUT)) return r;
+    }
+    WXH_HIP(wx::launch_layernorm(E->x, wx::DT_F32, d, nullptr, 0, nullptr, 0, W.ln2_g,
+                                 W.ln2_b, 1e-5f, E->aq, wx::DT_I8, d, M, d, false, s,
+                                 E->asc));
+    if (int r = mark(ST_LN)) return r;
+    {
+      wx::EpiParams e;
+      e.out = E->f32ws;
+      e.ldo = ffn;
+      e.bias = W.b1;
+      if (int r = gemm(M, ffn, d, W.w1_q, W.s1, wx::EPI_F32_GELU, e)) return r;
+      if (int r = mark(ST_FC1)) return r;
+    }
+    {
+      WXH_HIP(wx::launch_quantize_rows(E->f32ws, wx::DT_F32, ffn, M, ffn, E->aq, ffn, ffn,
+                                       E->asc, false, s));
+      wx::EpiParams e;
+      e.out = E->x;
+      e.ldo = d;
+      e.bias = W.b2;
+      if (int r = gemm(M, d, ffn, W.w2_q, W.s2, wx::EPI_RESID, e)) return r;
+      if (int r = mark(ST_FC2)) return r;
+    }
+  }
+  return WXH_OK;
+}
+
 int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* timer) {
+  if (E->i8) return run_body_i8(E, batch, frames, s, timer);
   const auto& D = E->dims;
   const int d = D.d_model, nh = D.n_head, T = frames;
   const int ctx = (T - 1) / 2 + 1;
@@ -665,9 +882,13 @@ int forward_impl(wxh_encoder* E, const float* mel, int batch, int frames, float*
   const auto& D = E->dims;
   const int ctx = (frames - 1) / 2 + 1;
   if (int r = ensure_workspace(E, batch, frames)) return r;
-  WXH_HIP(wx::launch_prep_mel(mel, batch, D.n_mels, frames, E->melT, s));
-  zero_pad_rows_kernel<<<batch, 256, 0, s>>>(E->x1, frames, D.d_model);
-  WXH_HIP(hipGetLastError());
+  if (E->i8) {
+    WXH_HIP(wx::launch_transpose_f32(mel, batch, D.n_mels, frames, E->f32ws, s));
+  } else {
+    WXH_HIP(wx::launch_prep_mel(mel, batch, D.n_mels, frames, E->melT, s));
+    zero_pad_rows_kernel<<<batch, 256, 0, s>>>(E->x1, frames, D.d_model);
+    WXH_HIP(hipGetLastError());
+  }
   if (timer) {
     hipEvent_t ev;
     WXH_HIP(hipEventCreate(&ev));
@@ -804,8 +1025,10 @@ int wxh_encoder_set_weight(wxh_encoder* E, const char* name, const float* host,
       for (int64_t c = 0; c < cin; ++c)
         for (int64_t j = 0; j < 3; ++j)
           perm[(size_t)o * 3 * cin + j * cin + c] = host[(o * cin + c) * 3 + j];
-    r = upload_bf16(E, n == "conv1.weight" ? E->conv1_w : E->conv2_w, perm.data(),
-                    (int)d, (int)(3 * cin));
+    const bool c1 = n == "conv1.weight";
+    r = upload_bf16(E, c1 ? E->conv1_w : E->conv2_w, perm.data(), (int)d, (int)(3 * cin),
+                    E->i8_weights ? (c1 ? E->conv1_q : E->conv2_q) : nullptr,
+                    c1 ? E->conv1_s : E->conv2_s, c1 ? E->k1p : (int)(3 * d));
   } else if (n == "conv1.bias" || n == "conv2.bias" || n == "ln_post.weight" ||
              n == "ln_post.bias") {
     if (!shape_is(shape, ndim, {d})) return bad_shape();
@@ -828,19 +1051,24 @@ int wxh_encoder_set_weight(wxh_encoder* E, const char* name, const float* host,
     if (t == "attn.query.weight" || t == "attn.key.weight" || t == "attn.value.weight") {
       if (!shape_is(shape, ndim, {d, d})) return bad_shape();
       const int part = t == "attn.query.weight" ? 0 : t == "attn.key.weight" ? 1 : 2;
-      r = upload_bf16(E, W.wqkv + (size_t)part * d * d, host, (int)d, (int)d);
+      r = upload_bf16(E, W.wqkv + (size_t)part * d * d, host, (int)d, (int)d,
+                      E->i8_weights ? W.wqkv_q + (size_t)part * d * d : nullptr,
+                      W.sqkv + part * d, (int)d);
     } else if (t == "attn.query.bias" || t == "attn.value.bias") {
       if (!shape_is(shape, ndim, {d})) return bad_shape();
       r = upload_f32(E, W.bqkv + (t == "attn.query.bias" ? 0 : 2 * d), host, d);
     } else if (t == "attn.out.weight") {
       if (!shape_is(shape, ndim, {d, d})) return bad_shape();
-      r = upload_bf16(E, W.wo, host, (int)d, (int)d);
+      r = upload_bf16(E, W.wo, host, (int)d, (int)d, E->i8_weights ? W.wo_q : nullptr, W.so,
+                      (int)d);
     } else if (t == "mlp.0.weight") {
       if (!shape_is(shape, ndim, {ffn, d})) return bad_shape();
-      r = upload_bf16(E, W.w1, host, (int)ffn, (int)d);
+      r = upload_bf16(E, W.w1, host, (int)ffn, (int)d, E->i8_weights ? W.w1_q : nullptr, W.s1,
+                      (int)d);
     } else if (t == "mlp.2.weight") {
       if (!shape_is(shape, ndim, {d, ffn})) return bad_shape();
-      r = upload_bf16(E, W.w2, host, (int)d, (int)ffn);
+      r = upload_bf16(E, W.w2, host, (int)d, (int)ffn, E->i8_weights ? W.w2_q : nullptr, W.s2,
+                      (int)ffn);
     } else if (t == "mlp.0.bias") {
       if (!shape_is(shape, ndim, {ffn})) return bad_shape();
       r = upload_f32(E, W.b1, host, ffn);
@@ -874,6 +1102,53 @@ int wxh_encoder_ready(wxh_encoder* E) {
 int wxh_encoder_set_graph(wxh_encoder* E, int enabled) {
   WXH_REQUIRE(E, "wxh_encoder_set_graph: null handle");
   E->use_graph = enabled != 0;
+  return WXH_OK;
+}
+
+int wxh_encoder_enable_int8(wxh_encoder* E) {
+  WXH_REQUIRE(E, "wxh_encoder_enable_int8: null handle");
+  if (E->i8_weights) return WXH_OK;
+  const auto& D = E->dims;
+  if (!E->have.empty())
+    return fail(WXH_ERR_STATE, "wxh_encoder_enable_int8: call it before setting weights");
+  if (D.d_model % wx::kI8KAlign != 0)
+    return fail(WXH_ERR_UNSUPPORTED, "wxh_encoder_enable_int8: d_model=%d is not a multiple "
+                "of %d", D.d_model, wx::kI8KAlign);
+  if (D.mlp_gelu != WXH_GELU_ERF)
+    return fail(WXH_ERR_UNSUPPORTED, "wxh_encoder_enable_int8: needs the erf MLP GELU");
+  const int d = D.d_model, ffn = E->ffn;
+  E->k1p = (3 * D.n_mels + wx::kI8KAlign - 1) / wx::kI8KAlign * wx::kI8KAlign;
+  auto& A = E->allocs;
+  int r = WXH_OK;
+  r = r ? r : dalloc(A, &E->conv1_q, (size_t)d * E->k1p, true);
+  r = r ? r : dalloc(A, &E->conv2_q, (size_t)d * 3 * d, true);
+  r = r ? r : dalloc(A, &E->conv1_s, d, true);
+  r = r ? r : dalloc(A, &E->conv2_s, d, true);
+  for (auto& W : E->layers) {
+    r = r ? r : dalloc(A, &W.wqkv_q, (size_t)3 * d * d, true);
+    r = r ? r : dalloc(A, &W.wo_q, (size_t)d * d, true);
+    r = r ? r : dalloc(A, &W.w1_q, (size_t)ffn * d, true);
+    r = r ? r : dalloc(A, &W.w2_q, (size_t)d * ffn, true);
+    r = r ? r : dalloc(A, &W.sqkv, 3 * d, true);
+    r = r ? r : dalloc(A, &W.so, d, true);
+    r = r ? r : dalloc(A, &W.s1, ffn, true);
+    r = r ? r : dalloc(A, &W.s2, d, true);
+  }
+  if (r != WXH_OK) return r;
+  E->i8_weights = true;
+  return WXH_OK;
+}
+
+int wxh_encoder_set_int8(wxh_encoder* E, int on) {
+  WXH_REQUIRE(E, "wxh_encoder_set_int8: null handle");
+  if (on && !E->i8_weights)
+    return fail(WXH_ERR_STATE, "wxh_encoder_set_int8: wxh_encoder_enable_int8 was not called "
+                "before the weights were set");
+  if ((on != 0) != E->i8) {
+    (void)hipStreamSynchronize(E->ctx->stream);
+    drop_graphs(E);
+    E->i8 = on != 0;
+  }
   return WXH_OK;
 }
 

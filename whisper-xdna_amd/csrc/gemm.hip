@@ -1,8 +1,12 @@
-// bf16 x bf16 -> fp32 MFMA GEMM for gfx950: C[M,N] = A[M,K] . W[N,K]^T.
+// bf16 x bf16 -> fp32 MFMA GEMM for gfx950: C[M,N] = A[M,K] . W[N,K]^T, and
+// its int8 x int8 -> int32 variant (launch_gemm_i8) with per-row and
+// per-column scales.
 //
 // Replaces the MLIR-AIE whole_array GEMM the reference drives through
 // RawRT.matmul / mm_start / mm_finish (src/rawxrt.py:926-996) and the conv
-// front end's im2col GEMMs (src/npu_whisper_encoder.py:422-454).
+// front end's im2col GEMMs (src/npu_whisper_encoder.py:422-454); the int8
+// variant computes the reference's quantised matmul
+// (bench/probe_int8_decode.py:48-74) on the device.
 //
 // Both operands are K-contiguous (activations row-major, weights in torch's
 // (out, in) layout), so every MFMA fragment is one 16-byte LDS read. Tiles are
@@ -337,7 +341,8 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(int M, int N, int K,
     int m = bm0 + r;
     m = m < M ? m : M - 1;
     const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
-    ap[i] = a.ptr + (int64_t)b * a.batch_stride + (int64_t)t * a.lda + kc;
+    ap[i] = static_cast<const uint16_t*>(a.ptr) + (int64_t)b * a.batch_stride +
+            (int64_t)t * a.lda + kc;
     aoff[i] = r * C::LDK + kc;
     akc[i] = kc;
   }
@@ -542,7 +547,7 @@ __device__ __forceinline__ void sk_store(__amdgpu_buffer_rsrc_t ws, int64_t base
           for (int r = 0; r < 4; ++r)
             if (n0 + r < N)
               __builtin_amdgcn_raw_buffer_store_b32(
-                  __builtin_bit_cast(uint32_t, acc[i][j][g * 4 + r]), ws,
+                  __float_as_uint(acc[i][j][g * 4 + r]), ws,
                   (int)((rb + n0 + r) * 4), 0, kCpolSc1);
         }
       });
@@ -732,9 +737,16 @@ __device__ __forceinline__ void epi_lds_f32(const EpiParams& e, const f32x16 (&a
   });
 }
 
-template <class C, int MODE>
+// I8: int8 operands (K-step of 2 BK elements: the same bytes per row as
+// bf16), v_mfma_i32_32x32x32_i8 into int32 accumulators held in the same
+// registers, converted and scaled (a_scale per row, w_scale per column)
+// after the main loop. The v_mfma_i32_32x32x32_i8 operands are 16 bytes per
+// lane like the bf16 ones, and A and W fragments are read with the same
+// lane -> K mapping, so the exact integer dot product does not depend on
+// how the instruction orders K inside a 32-wide slice.
+template <class C, int MODE, bool I8>
 __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, GemmA a,
-                                                         const uint16_t* __restrict__ W,
+                                                         const void* __restrict__ W,
                                                          int64_t ldw, EpiParams e,
                                                          int a_bytes, int w_bytes, int group_m,
                                                          int remap) {
@@ -770,8 +782,12 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   const int tn = (pid % width) / gsz;
   const int bm0 = tm * C::BM, bn0 = tn * C::BN;
 
-  const auto ra = __builtin_amdgcn_make_buffer_rsrc((void*)a.ptr, (short)0, a_bytes, 0x00020000);
-  const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, w_bytes, 0x00020000);
+  const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.ptr), (short)0, a_bytes,
+                                                    0x00020000);
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(W), (short)0, w_bytes,
+                                                    0x00020000);
+  constexpr int ES = I8 ? 1 : 2;            // bytes per element
+  constexpr int BKE = C::ROWB / ES;         // K elements per step
 
   // lane -> tile row within its DMA block and the logical chunk that belongs
   // in its slot (lane % CPR) under the swizzle
@@ -784,7 +800,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     int m = bm0 + row;
     m = m < M ? m : M - 1;
     const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
-    aoff[j] = (uint32_t)(((int64_t)b * a.batch_stride + (int64_t)t * a.lda + lchunk * 8) * 2);
+    aoff[j] = (uint32_t)(((int64_t)b * a.batch_stride + (int64_t)t * a.lda) * ES + lchunk * 16);
   }
 #pragma unroll
   for (int j = 0; j < C::B_INSTR; ++j) {
@@ -792,11 +808,11 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     const int lchunk = (lane % C::CPR) ^ ((row / C::RPW) % C::CPR);
     int n = bn0 + row;
     n = n < N ? n : N - 1;
-    boff[j] = (uint32_t)(((int64_t)n * ldw + lchunk * 8) * 2);
+    boff[j] = (uint32_t)((int64_t)n * ldw * ES + lchunk * 16);
   }
   auto issue = [&](int kt) {
     uint8_t* base = smem + (kt % C::S) * C::STAGE;
-    const int soff = (kbase + kt * C::BK) * 2;
+    const int soff = (kbase + kt * BKE) * ES;
 #pragma unroll
     for (int j = 0; j < C::A_INSTR; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -819,7 +835,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   f32x4 bv[C::TN][4];
   load_bias<C::TN>(e.bias, N, bn0 + wn * C::WTN, lane, bv);
 
-  const int nk = ksplit / C::BK;
+  const int nk = ksplit / BKE;
   const int sw = (l32 / C::RPW) % C::CPR;  // the swizzle of every row this lane reads
   const int arow = (wm * C::WTM + l32) * C::ROWB;
   const int brow = (wn * C::WTN + l32) * C::ROWB;
@@ -840,8 +856,15 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   auto mfmas = [&](int set) {
     static_for<C::TM>([&](auto i) {
       static_for<C::TN>([&](auto j) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[set][j], af[set][i],
-                                                            acc[i][j], 0, 0, 0);
+        if constexpr (I8)
+          acc[i][j] = __builtin_bit_cast(
+              f32x16, __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                          __builtin_bit_cast(i32x4, bfr[set][j]),
+                          __builtin_bit_cast(i32x4, af[set][i]),
+                          __builtin_bit_cast(i32x16, acc[i][j]), 0, 0, 0));
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[set][j], af[set][i],
+                                                              acc[i][j], 0, 0, 0);
       });
     });
   };
@@ -903,7 +926,42 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   for (; kt + 1 < nk; ++kt) step(kt, F_{}, T_{});
   if (kt < nk) step(kt, F_{}, F_{});
 
-  if (splits > 1) {
+  if constexpr (I8) {
+    // int32 sums -> fp32 (RNE), times the row's and the column's scale, in
+    // that order, each product rounded: contraction is off here, so the
+    // second product cannot be fused with the epilogue's bias add into one
+    // FMA (the reference rounds r * sa * sw before adding the bias; fused,
+    // 6 of 7.7M fc1-shaped GELU inputs came out 1-2 ulp off). An element's
+    // bits are taken with __float_as_int (a value): __builtin_bit_cast of an
+    // ext-vector element lvalue reads element 0 with this compiler.
+#pragma clang fp contract(off)
+    const int row0 = bm0 + wm * C::WTM, col0 = bn0 + wn * C::WTN;
+    float sa[C::TM];
+    static_for<C::TM>([&](auto i) {
+      const int m = row0 + i * 32 + l32;
+      sa[i] = m < M ? e.a_scale[m] : 0.f;
+    });
+    const bool vec = ((uintptr_t)e.w_scale & 15) == 0 && col0 + C::TN * 32 <= N;
+    static_for<C::TN>([&](auto j) {
+      static_for<4>([&](auto g) {
+        const int n0 = col0 + j * 32 + g * 8 + half * 4;
+        f32x4 sw;
+        if (vec) {
+          sw = *reinterpret_cast<const f32x4*>(e.w_scale + n0);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sw[r] = n0 + r < N ? e.w_scale[n0 + r] : 0.f;
+        }
+        static_for<C::TM>([&](auto i) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[i][j][g * 4 + r] =
+                ((float)__float_as_int(acc[i][j][g * 4 + r]) * sa[i]) * sw[r];
+        });
+      });
+    });
+  }
+  if (!I8 && splits > 1) {
     // Publish this split's partial, then count the tile's finished splits;
     // the last one sums them and runs the epilogue. No workgroup waits on
     // another, so any dispatch order completes. The flag lives in the ring's
@@ -929,35 +987,53 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     if (tid == 0)  // ready for the next launch
       __hip_atomic_store(e.sk_cnt + tile_id, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  // EPI_F32_GELU: bias and GELU applied to the accumulators in place, then
+  // the plain fp32 epilogue with a zero bias (GELU inside the staged
+  // epilogue's unrolled loop would hold its temporaries next to every
+  // accumulator and spill)
+  constexpr int EMODE = MODE == EPI_F32_GELU ? EPI_F32 : MODE;
+  if constexpr (MODE == EPI_F32_GELU) {
+    static_for<C::TN>([&](auto j) {
+      static_for<4>([&](auto g) {
+        static_for<C::TM>([&](auto i) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[i][j][g * 4 + r] = gelu_erf(acc[i][j][g * 4 + r] + bv[j][g][r]);
+        });
+        bv[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      });
+    });
+  }
   // Staged epilogues (conditions uniform over the workgroup; the ring is
   // idle once every wave is past the main loop's last barrier: DMA drained,
   // fragment reads done).
   if (bm0 + C::BM <= M && bn0 + C::BN <= N) {
-    if constexpr (MODE == EPI_BF16) {
+    if constexpr (EMODE == EPI_BF16) {
       if ((e.ldo & 7) == 0 && ((uintptr_t)e.out & 15) == 0) {
         epi_lds_bf16<C>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
         return;
       }
     }
-    if constexpr (MODE == EPI_QKV) {
+    if constexpr (EMODE == EPI_QKV) {
       if (bn0 < 2 * e.d_model && e.d_model % C::BN == 0) {
         epi_lds_qk<C>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
         return;
       }
     }
-    if constexpr (MODE == EPI_F32 || MODE == EPI_RESID) {
+    if constexpr (EMODE == EPI_F32 || EMODE == EPI_RESID) {
       if ((e.ldo & 3) == 0 && ((uintptr_t)e.out & 15) == 0) {
-        epi_lds_f32<C, MODE>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
+        epi_lds_f32<C, EMODE>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
         return;
       }
     }
   }
-  store_tile_t<MODE, C::TM, C::TN>(e, acc, bv, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN, lane);
+  store_tile_t<EMODE, C::TM, C::TN>(e, acc, bv, M, N, bm0 + wm * C::WTM, bn0 + wn * C::WTN,
+                                    lane);
 #endif
 }
 
-template <class C>
-static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const uint16_t* W,
+template <class C, bool I8 = false>
+static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const void* W,
                                   int64_t ldw, int mode, const EpiParams& e,
                                   int a_bytes, int w_bytes, hipStream_t s) {
   const int tiles = ((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
@@ -981,16 +1057,26 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const uin
   }
 #define WX_DMA(MD)                                                                   \
   case MD:                                                                           \
-    gemm_dma_kernel<C, MD><<<grid, block, 0, s>>>(M, N, K, a, W, ldw, e, a_bytes,   \
-                                                  w_bytes, group_m, remap);          \
+    gemm_dma_kernel<C, MD, I8><<<grid, block, 0, s>>>(M, N, K, a, W, ldw, e, a_bytes, \
+                                                      w_bytes, group_m, remap);      \
     break;
   if (mode == EPI_BF16 && e.gelu == GELU_ERF) mode = EPI_BF16_GELU;
   if (mode == EPI_BF16 && e.gelu == GELU_POLY4_RNE) mode = EPI_BF16_POLY4;
-  switch (mode) {
-    WX_DMA(EPI_F32) WX_DMA(EPI_BF16) WX_DMA(EPI_RESID) WX_DMA(EPI_CONV1)
-    WX_DMA(EPI_CONV2) WX_DMA(EPI_QKV) WX_DMA(EPI_BF16_GELU) WX_DMA(EPI_BF16_POLY4)
-    default:
-      return hipErrorInvalidValue;
+  if constexpr (I8) {
+    // the int8 encoder's and the C ABI's epilogues
+    switch (mode) {
+      WX_DMA(EPI_F32) WX_DMA(EPI_BF16) WX_DMA(EPI_RESID) WX_DMA(EPI_CONV2) WX_DMA(EPI_QKV)
+      WX_DMA(EPI_BF16_GELU) WX_DMA(EPI_F32_GELU)
+      default:
+        return hipErrorInvalidValue;
+    }
+  } else {
+    switch (mode) {
+      WX_DMA(EPI_F32) WX_DMA(EPI_BF16) WX_DMA(EPI_RESID) WX_DMA(EPI_CONV1)
+      WX_DMA(EPI_CONV2) WX_DMA(EPI_QKV) WX_DMA(EPI_BF16_GELU) WX_DMA(EPI_BF16_POLY4)
+      default:
+        return hipErrorInvalidValue;
+    }
   }
 #undef WX_DMA
   return hipGetLastError();
@@ -999,7 +1085,7 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const uin
 // Byte extent of A that rows [0, M) can touch (the buffer descriptor's
 // range); the largest row offset is that of the last row of the last batch
 // item or of the first batch item's last row.
-static int64_t a_extent_bytes(int M, int K, const GemmA& a) {
+static int64_t a_extent_bytes(int M, int K, const GemmA& a, int es = 2) {
   auto off = [&](int m) {
     const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
     return (int64_t)b * a.batch_stride + (int64_t)t * a.lda;
@@ -1008,7 +1094,7 @@ static int64_t a_extent_bytes(int M, int K, const GemmA& a) {
   int64_t hi = off(M - 1);
   const int64_t h2 = off(last_first);
   if (h2 > hi) hi = h2;
-  return (hi + K) * 2;
+  return (hi + K) * es;
 }
 
 // Split count for a launch of `tiles` 128x128 tiles at one workgroup per
@@ -1088,6 +1174,32 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
     return gemm_dma_launch<T128w8s3>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
   }
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+}
+
+// Same tile choice as launch_gemm (the K-step covers 128 int8 elements, the
+// bytes of a bf16 step); no split-K, whose fp32 partial sums would not be
+// the exact integer sum.
+hipError_t launch_gemm_i8(int M, int N, int K, const GemmA& a, const int8_t* W, int64_t ldw,
+                          int mode, const EpiParams& e_in, hipStream_t s) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  EpiParams e = e_in;
+  e.splits = 1;
+  const int64_t ab = a_extent_bytes(M, K, a, 1);
+  const int64_t wb = (int64_t)(N - 1) * ldw + K;
+  if (K <= 0 || K % kI8KAlign || a.lda % 16 || ldw % 16 || a.batch_stride % 16 ||
+      ((uintptr_t)a.ptr & 15) || ((uintptr_t)W & 15) || ab >= (1ll << 31) ||
+      wb >= (1ll << 31) || !e.a_scale || !e.w_scale)
+    return hipErrorInvalidValue;
+  using T128 = DCfg<128, 128, 2, 2, 64, 2>;
+  using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
+  using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
+  const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  if (big_tiles >= 256)
+    return gemm_dma_launch<T256w8, true>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  if (tiles128 <= 256)
+    return gemm_dma_launch<T128w8s3, true>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  return gemm_dma_launch<T128, true>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
 }
 
 }  // namespace wx

@@ -11,18 +11,21 @@
 
 namespace wx {
 
-enum DType { DT_BF16 = 0, DT_F32 = 1 };
+enum DType { DT_BF16 = 0, DT_F32 = 1, DT_I8 = 2 };
 enum Gelu { GELU_NONE = -1, GELU_ERF = 0, GELU_POLY4_RNE = 1, GELU_POLY4_TRUNC = 2 };
 
 // ---------------------------------------------------------------- row ops
 // y = LN(x [+ resid]) * gamma + beta over each row of `cols` elements.
 // sum_out (fp32, optional) receives x + resid before normalisation.
 // stream: non-temporal loads and stores (for rows nothing reads again soon).
+// y_dtype DT_I8: y is the row quantised per row (launch_quantize_rows'
+// rule, on the fp32 LN output) with its scale in y_scale[row].
 hipError_t launch_layernorm(const void* x, int x_dtype, int64_t ldx,
                             const float* resid, int64_t ldr, float* sum_out,
                             int64_t lds, const float* gamma, const float* beta,
                             float eps, void* y, int y_dtype, int64_t ldy,
-                            int rows, int cols, bool stream, hipStream_t s);
+                            int rows, int cols, bool stream, hipStream_t s,
+                            float* y_scale = nullptr);
 
 // Max row width the one-wave-per-row LayerNorm and softmax keep in registers.
 constexpr int kMaxRowCols = 4096;
@@ -61,10 +64,11 @@ enum EpiMode {
   // from EpiParams::gelu; callers pass EPI_BF16)
   EPI_BF16_GELU = 6,   // out bf16 = gelu_erf(acc + bias)
   EPI_BF16_POLY4 = 7,  // out bf16 = poly4 GELU (g4f) of acc + bias
+  EPI_F32_GELU = 8,    // out fp32 = gelu_erf(acc + bias)
 };
 
 struct GemmA {
-  const uint16_t* ptr;
+  const void* ptr;  // bf16 (launch_gemm) or int8 (launch_gemm_i8) elements
   int64_t lda;
   int rows_per_batch;
   int64_t batch_stride;
@@ -95,11 +99,43 @@ struct EpiParams {
   unsigned* sk_cnt = nullptr;
   int sk_cnt_len = 0;
   int splits = 1;                  // set by launch_gemm
+  // launch_gemm_i8: acc (int32) becomes (float(acc) * a_scale[row]) *
+  // w_scale[col] before the bias and the epilogue
+  const float* a_scale = nullptr;
+  const float* w_scale = nullptr;
 };
 
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
                        int64_t ldw, int mode, const EpiParams& e,
                        hipStream_t s);
+
+// int8 x int8 -> int32 MFMA GEMM with the same epilogues (no split-K): A
+// int8 [M, K] with a per-row scale, W int8 [N, K] with a per-column scale.
+// K % 128 == 0, lda, ldw and the batch stride multiples of 16 bytes, A and W
+// 16-byte aligned (callers zero-pad K).
+constexpr int kI8KAlign = 128;
+hipError_t launch_gemm_i8(int M, int N, int K, const GemmA& a, const int8_t* W,
+                          int64_t ldw, int mode, const EpiParams& e, hipStream_t s);
+
+// ---------------------------------------------------------------- int8 quantisation
+// Per-row symmetric quantisation: scale = max|x_row| / 127 (1 if the row is
+// all zero), q = rint(x / scale) as int8, columns [cols, cols_pad) zero.
+// given: scale[0] is supplied (one scale for every row) instead of computed.
+hipError_t launch_quantize_rows(const void* x, int x_dtype, int64_t ldx, int rows, int cols,
+                                int8_t* q, int64_t ldq, int cols_pad, float* scale,
+                                bool given, hipStream_t s);
+// out[0] = max|x| / 127 over a rows x cols band (1 if all zero)
+hipError_t launch_absmax_scale(const void* x, int x_dtype, int64_t ldx, int rows, int cols,
+                               float* out, unsigned* scratch, hipStream_t s);
+// im2col of a conv1d (kernel 3, padding 1) over fp32 rows x [B, T_in, C],
+// quantised per output row: row (b, t) is [x[s t - 1], x[s t], x[s t + 1]]
+// (tap-major, rows outside [0, T_in) zero), padded with zeros to ldq.
+hipError_t launch_im2col_quant(const float* x, int batch, int T_in, int C, int stride,
+                               int T_out, int8_t* q, int64_t ldq, float* scale,
+                               hipStream_t s);
+// fp32 [B, C, T] -> fp32 [B, T, C]
+hipError_t launch_transpose_f32(const float* x, int batch, int C, int T, float* y,
+                                hipStream_t s);
 
 // ---------------------------------------------------------------- attention
 // Head dimension is fixed at 64 (Whisper: n_head = d_model / 64).

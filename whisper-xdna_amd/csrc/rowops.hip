@@ -73,12 +73,15 @@ struct LnRow {
   }
 };
 
-// LayerNorm of one row from its loaded chunks; gb = gamma [cols], beta [cols]
-template <int NCH, bool XF32, bool YF32, bool RESID, bool STREAM>
+// LayerNorm of one row from its loaded chunks; gb = gamma [cols], beta [cols].
+// YT: DT_BF16, DT_F32, or DT_I8 (the fp32 result quantised per row:
+// scale = max|y| / 127, or 1 for an all-zero row, q = rint(y / scale); the
+// scale goes to ysc[row])
+template <int NCH, bool XF32, int YT, bool RESID, bool STREAM>
 __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cur,
                                        const float* gb, float* __restrict__ sp, int64_t lds,
                                        float eps, void* __restrict__ yp, int64_t ldy, int row,
-                                       int lane, int cols) {
+                                       int lane, int cols, float* __restrict__ ysc) {
   auto st = [](auto v, auto* p) {
     if (STREAM) __builtin_nontemporal_store(v, p); else *p = v;
   };
@@ -133,6 +136,42 @@ __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cu
   }
   const float var = wave_sum(sq) * inv_n;
   const float rstd = 1.0f / sqrtf(var + eps);
+  if constexpr (YT == DT_I8) {
+    float m = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int ch = lane + c * 64;
+      if (ch >= nch) continue;
+      const int64_t col = (int64_t)ch * 8;
+      const f32x4* g = reinterpret_cast<const f32x4*>(gb + col);
+      const f32x4* bb = reinterpret_cast<const f32x4*>(gb + cols + col);
+      const f32x4 g0 = g[0], g1 = g[1], b0 = bb[0], b1 = bb[1];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[c][j] = (v[c][j] - mean) * rstd * g0[j] + b0[j];
+        v[c][j + 4] = (v[c][j + 4] - mean) * rstd * g1[j] + b1[j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[c][j]));
+    }
+    m = wave_max(m) / 127.0f;
+    const float sc = m == 0.f ? 1.0f : m;
+    if (lane == 0) ysc[row] = sc;
+    auto q4 = [&](const float* a) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w |= (uint32_t)((int)rintf(a[j] / sc) & 0xFF) << (8 * j);
+      return w;
+    };
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int ch = lane + c * 64;
+      if (ch >= nch) continue;
+      int8_t* y = static_cast<int8_t*>(yp) + row * ldy + (int64_t)ch * 8;
+      st(u32x2{q4(&v[c][0]), q4(&v[c][4])}, reinterpret_cast<u32x2*>(y));
+    }
+    return;
+  }
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int ch = lane + c * 64;
@@ -147,7 +186,7 @@ __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cu
       o[j] = (v[c][j] - mean) * rstd * g0[j] + b0[j];
       o[j + 4] = (v[c][j + 4] - mean) * rstd * g1[j] + b1[j];
     }
-    if (YF32) {
+    if (YT == DT_F32) {
       float* y = static_cast<float*>(yp) + row * ldy + col;
       st(f32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<f32x4*>(y));
       st(f32x4{o[4], o[5], o[6], o[7]}, reinterpret_cast<f32x4*>(y + 4));
@@ -159,12 +198,12 @@ __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cu
   }
 }
 
-template <int NCH, bool XF32, bool YF32, bool RESID, bool STREAM>
+template <int NCH, bool XF32, int YT, bool RESID, bool STREAM>
 __global__ __launch_bounds__(256) void ln_kernel(
     const void* __restrict__ xp, int64_t ldx, const float* __restrict__ rp,
     int64_t ldr, float* __restrict__ sp, int64_t lds,
     const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
-    void* __restrict__ yp, int64_t ldy, int rows, int cols) {
+    void* __restrict__ yp, int64_t ldy, int rows, int cols, float* __restrict__ ysc) {
   extern __shared__ __align__(16) float ln_gb[];  // gamma [cols], beta [cols]
   // wave-uniform; readfirstlane keeps it (and the descriptor lengths made
   // from it) in scalar registers: cols is also read in the divergent loop
@@ -210,11 +249,13 @@ __global__ __launch_bounds__(256) void ln_kernel(
   __syncthreads();
   while (row < rows) {
     rb.load(xp, ldx, rp, ldr, row + waves, rows, lane, cols4);
-    ln_row<NCH, XF32, YF32, RESID, STREAM>(ra, ln_gb, sp, lds, eps, yp, ldy, row, lane, cols);
+    ln_row<NCH, XF32, YT, RESID, STREAM>(ra, ln_gb, sp, lds, eps, yp, ldy, row, lane, cols,
+                                         ysc);
     row += waves;
     if (row >= rows) break;
     ra.load(xp, ldx, rp, ldr, row + waves, rows, lane, cols4);
-    ln_row<NCH, XF32, YF32, RESID, STREAM>(rb, ln_gb, sp, lds, eps, yp, ldy, row, lane, cols);
+    ln_row<NCH, XF32, YT, RESID, STREAM>(rb, ln_gb, sp, lds, eps, yp, ldy, row, lane, cols,
+                                         ysc);
     row += waves;
   }
 }
@@ -229,24 +270,33 @@ static hipError_t ln_dispatch(const void* x, int x_dtype, int64_t ldx,
                               int64_t lds, const float* gamma,
                               const float* beta, float eps, void* y,
                               int y_dtype, int64_t ldy, int rows, int cols,
-                              bool stream, hipStream_t s) {
+                              bool stream, hipStream_t s, float* ysc) {
   dim3 grid(std::min((rows + 3) / 4, kLnGrid)), block(256);
   const size_t smem = 2 * (size_t)cols * sizeof(float);
-  const bool xf = x_dtype == DT_F32, yf = y_dtype == DT_F32, r = resid != nullptr;
-#define WX_LN(XF, YF, R)                                                             \
-  if (xf == XF && yf == YF && r == R) {                                              \
+  const bool xf = x_dtype == DT_F32, r = resid != nullptr;
+  const int yt = y_dtype;
+  if (yt == DT_I8) {
+    // the int8 encoder's LayerNorm only: fp32 residual stream in, no fused
+    // residual add, cached stores
+    if (!xf || r || stream) return hipErrorInvalidValue;
+    ln_kernel<NCH, true, DT_I8, false, false><<<grid, block, smem, s>>>(
+        x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols, ysc);
+    return hipGetLastError();
+  }
+#define WX_LN(XF, YT, R)                                                             \
+  if (xf == XF && yt == YT && r == R) {                                              \
     if (stream)                                                                      \
-      ln_kernel<NCH, XF, YF, R, true><<<grid, block, smem, s>>>(                     \
-          x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols);   \
+      ln_kernel<NCH, XF, YT, R, true><<<grid, block, smem, s>>>(                     \
+          x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols, ysc); \
     else                                                                             \
-      ln_kernel<NCH, XF, YF, R, false><<<grid, block, smem, s>>>(                    \
-          x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols);   \
+      ln_kernel<NCH, XF, YT, R, false><<<grid, block, smem, s>>>(                    \
+          x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols, ysc); \
     return hipGetLastError();                                                        \
   }
-  WX_LN(false, false, false) WX_LN(false, true, false)
-  WX_LN(true, false, false) WX_LN(true, true, false)
-  WX_LN(false, false, true) WX_LN(false, true, true)
-  WX_LN(true, false, true) WX_LN(true, true, true)
+  WX_LN(false, DT_BF16, false) WX_LN(false, DT_F32, false)
+  WX_LN(true, DT_BF16, false) WX_LN(true, DT_F32, false)
+  WX_LN(false, DT_BF16, true) WX_LN(false, DT_F32, true)
+  WX_LN(true, DT_BF16, true) WX_LN(true, DT_F32, true)
 #undef WX_LN
   return hipErrorInvalidValue;
 }
@@ -255,14 +305,15 @@ hipError_t launch_layernorm(const void* x, int x_dtype, int64_t ldx,
                             const float* resid, int64_t ldr, float* sum_out,
                             int64_t lds, const float* gamma, const float* beta,
                             float eps, void* y, int y_dtype, int64_t ldy,
-                            int rows, int cols, bool stream, hipStream_t s) {
+                            int rows, int cols, bool stream, hipStream_t s,
+                            float* y_scale) {
   if (rows <= 0) return hipSuccess;
   // chunks of 8 per lane: 64 lanes x 8 = 512 columns per chunk
   switch ((cols + 511) / 512) {
 #define WX_LNC(N)                                                                   \
     case N:                                                                         \
       return ln_dispatch<N>(x, x_dtype, ldx, resid, ldr, sum_out, lds, gamma, beta, \
-                            eps, y, y_dtype, ldy, rows, cols, stream, s);
+                            eps, y, y_dtype, ldy, rows, cols, stream, s, y_scale);
     WX_LNC(1) WX_LNC(2) WX_LNC(3) WX_LNC(4) WX_LNC(5) WX_LNC(6) WX_LNC(7) WX_LNC(8)
 #undef WX_LNC
   }

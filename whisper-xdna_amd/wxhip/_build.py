@@ -18,7 +18,7 @@ ROOT = PKG.parent
 CSRC = ROOT / "csrc"
 BUILD = ROOT / "_build"
 LIB = PKG / "libwxhip.so"
-SOURCES = ["rowops.hip", "gemm.hip", "attention.hip", "audio.hip", "capi.cpp"]
+SOURCES = ["rowops.hip", "gemm.hip", "attention.hip", "audio.hip", "quant.hip", "capi.cpp"]
 ARCH = "gfx950"
 # Per-file code generation options. The attention kernel feeds every MFMA
 # result straight into VALU work (softmax, rescaling), and the GEMM

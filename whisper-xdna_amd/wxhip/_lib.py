@@ -13,10 +13,10 @@ LIB_PATH = Path(__file__).resolve().with_name("libwxhip.so")
 
 WXH_OK, WXH_ERR_INVALID, WXH_ERR_HIP, WXH_ERR_INJECTED = 0, 1, 2, 3
 WXH_ERR_UNSUPPORTED, WXH_ERR_STATE = 4, 5
-WXH_BF16, WXH_F32 = 0, 1
+WXH_BF16, WXH_F32, WXH_I8 = 0, 1, 2
 WXH_GELU_ERF, WXH_GELU_POLY4_RNE, WXH_GELU_POLY4_TRUNC = 0, 1, 2
 WXH_EPI_F32, WXH_EPI_BF16, WXH_EPI_BF16_GELU_ERF = 0, 1, 2
-WXH_EPI_BF16_GELU_POLY4, WXH_EPI_RESID_F32 = 3, 4
+WXH_EPI_BF16_GELU_POLY4, WXH_EPI_RESID_F32, WXH_EPI_F32_GELU_ERF = 3, 4, 5
 WXH_FAIL_GEMM, WXH_FAIL_ATTN, WXH_FAIL_ROWOP, WXH_FAIL_ENCODER = 1, 2, 4, 8
 WXH_FAIL_FRONTEND = 16
 
@@ -60,6 +60,8 @@ SIGNATURES = {
     "wxh_softmax_rows": [P, P, I64, P, I64, I, I, P],
     "wxh_convert_f32_bf16": [P, P, I64, P, I64, I, I, I, P],
     "wxh_gemm_bf16": [P, I, I, I, P, I64, P, I64, P, P, I64, I, P],
+    "wxh_quantize_rows": [P, P, I, I64, I, I, P, I64, I, P, I, P],
+    "wxh_gemm_i8": [P, I, I, I, P, I64, P, P, I64, P, P, P, I64, I, P],
     "wxh_attention_padded_len": [I],
     "wxh_pack_qkv": [P, P, P, P, I64, I, I, I, P, P, P, P],
     "wxh_attention": [P, P, P, P, I, I, I, F, P, I, I64, P],
@@ -70,6 +72,8 @@ SIGNATURES = {
     "wxh_encoder_forward": [P, P, I, I, P, P],
     "wxh_encoder_forward_host": [P, P, I, I, P],
     "wxh_encoder_set_graph": [P, I],
+    "wxh_encoder_enable_int8": [P],
+    "wxh_encoder_set_int8": [P, I],
     "wxh_encoder_profile": [P, P, I, I, P, C.POINTER(C.c_float), I],
 }
 _RESTYPE = {"wxh_version": C.c_char_p, "wxh_last_error": C.c_char_p}

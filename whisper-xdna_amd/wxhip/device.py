@@ -191,6 +191,62 @@ class Device:
                _ld(W), _ptr(bias), _ptr(out), _ld(out), epilogue, self.stream())
         return out
 
+    # -- int8 ------------------------------------------------------------------
+    def quantize_rows(self, x, cols_pad=None, per_tensor=False, out=None, scale=None):
+        """Symmetric int8 quantisation of a 2-D x (fp32 or bf16), per row
+        (scale [rows]) or per tensor (scale [1]); see wxh_quantize_rows.
+        Returns (q int8 [rows, cols_pad], scale fp32)."""
+        torch = _torch()
+        self._check(x, (torch.float32, torch.bfloat16), "x", 2)
+        rows, cols = x.shape
+        cols_pad = cols if cols_pad is None else int(cols_pad)
+        if out is None:
+            out = torch.empty(rows, cols_pad, dtype=torch.int8, device=self.device)
+        self._check(out, torch.int8, "out", 2)
+        if tuple(out.shape) != (rows, cols_pad):
+            raise ValueError(f"out must be {(rows, cols_pad)}")
+        n = 1 if per_tensor else rows
+        if scale is None:
+            scale = torch.empty(n, dtype=torch.float32, device=self.device)
+        self._check(scale, torch.float32, "scale", 1)
+        if scale.numel() < n:
+            raise ValueError(f"scale needs {n} elements")
+        L.call("wxh_quantize_rows", self._h, _ptr(x), self._dt(x), _ld(x), rows, cols,
+               _ptr(out), _ld(out), cols_pad, _ptr(scale), int(bool(per_tensor)),
+               self.stream())
+        return out, scale
+
+    def gemm_i8(self, A, a_scale, W, w_scale, bias=None, epilogue=L.WXH_EPI_F32, out=None):
+        """int8 A [M,K] (row scales) . int8 W [N,K]^T (column scales) (+bias)
+        with a WXH_EPI_* epilogue; see wxh_gemm_i8."""
+        torch = _torch()
+        self._check(A, torch.int8, "A", 2)
+        self._check(W, torch.int8, "W", 2)
+        M, K = A.shape
+        N, K2 = W.shape
+        if K != K2:
+            raise ValueError(f"A {tuple(A.shape)} and W {tuple(W.shape)} disagree on K")
+        self._check(a_scale, torch.float32, "a_scale", 1)
+        self._check(w_scale, torch.float32, "w_scale", 1)
+        if a_scale.numel() < M or w_scale.numel() < N:
+            raise ValueError("a_scale needs M and w_scale N elements")
+        if bias is not None:
+            self._check(bias, torch.float32, "bias", 1)
+            if bias.numel() != N:
+                raise ValueError("bias must have N elements")
+        f32 = (L.WXH_EPI_F32, L.WXH_EPI_RESID_F32, L.WXH_EPI_F32_GELU_ERF)
+        odt = torch.float32 if epilogue in f32 else torch.bfloat16
+        if out is None:
+            if epilogue == L.WXH_EPI_RESID_F32:
+                raise ValueError("the residual epilogue needs out= (the fp32 residual)")
+            out = torch.empty(M, N, dtype=odt, device=self.device)
+        self._check(out, odt, "out", 2)
+        if tuple(out.shape) != (M, N):
+            raise ValueError(f"out must be {(M, N)}")
+        L.call("wxh_gemm_i8", self._h, M, N, K, _ptr(A), _ld(A), _ptr(a_scale), _ptr(W),
+               _ld(W), _ptr(w_scale), _ptr(bias), _ptr(out), _ld(out), epilogue, self.stream())
+        return out
+
     # -- attention -------------------------------------------------------------
     def padded_len(self, T):
         return self.lib.wxh_attention_padded_len(T)

@@ -153,7 +153,10 @@ def prepare_mlp_chunks(W, n_layer, d, chunk=0):
 
 def _runtime_of(fn):
     from .hiprt import HipRT
+    # a HipRT's matmul, or a plug that carries its HipRT (wxhip.int8.q_matmul_factory)
     rt = getattr(fn, "__self__", None)
+    if not isinstance(rt, HipRT):
+        rt = getattr(fn, "rt", None)
     if not isinstance(rt, HipRT):
         raise TypeError("encoder(): mm must be a HipRT's matmul (this build runs the "
                         "encoder on the GPU only; there is no numpy backend)")

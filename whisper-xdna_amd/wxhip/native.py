@@ -43,7 +43,7 @@ def weight_names(n_layer):
 class HipEncoder:
     """Whisper encoder on one GPU: weights resident, forward as a hipGraph."""
 
-    def __init__(self, dev, W, n_layer=None, mlp_gelu="erf", graph=True):
+    def __init__(self, dev, W, n_layer=None, mlp_gelu="erf", graph=True, int8=False):
         n_mels, d, n_head, nl, n_ctx = geometry(W)
         self.dev = dev
         self.n_mels, self.d_model, self.n_head, self.n_ctx = n_mels, d, n_head, n_ctx
@@ -57,9 +57,25 @@ class HipEncoder:
         h = C.c_void_p()
         L.call("wxh_encoder_create", dev.handle, C.byref(dims), C.byref(h))
         self._h = h
+        # int8: int8 copies of the GEMM weights are made while they upload
+        # (per output channel, from the fp32 values), and the forward runs
+        # the int8 GEMM path (wxh_encoder_set_int8); set_int8(False) goes
+        # back to bf16 with the same weights
+        self.int8_capable = bool(int8)
+        self.int8 = False
+        if int8:
+            L.call("wxh_encoder_enable_int8", self._h)
         self.load_weights(W)
+        if int8:
+            self.set_int8(True)
         if not graph:
             L.call("wxh_encoder_set_graph", self._h, 0)
+
+    def set_int8(self, on):
+        """Switch the forward between the int8 and the bf16 GEMM path (int8
+        needs the encoder built with int8=True)."""
+        L.call("wxh_encoder_set_int8", self._h, int(bool(on)))
+        self.int8 = bool(on)
 
     def load_weights(self, W):
         for name in weight_names(self.n_layer):
