@@ -2,7 +2,7 @@
 """Benchmark of the Whisper-encoder hot path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--no-rowops] [--workload l16|l1|l16s]
+                    [--no-rowops] [--no-int8] [--workload l16|l1|l16s]
 
 A step is one encoder forward (mel -> features) of the workload over inputs
 already resident in HBM, replayed as the captured hipGraph. Default workload:
@@ -12,8 +12,10 @@ The same run also reports the batch-1 latency (large-v3, ctx 1500), the
 encoder's fraction of the bf16 MFMA peak, per-stage device times (HIP events
 on the stream the kernels run on), the roofline of the dominant kernel, the
 row kernels' HBM throughput over rotating buffers larger than the 256 MB
-Infinity Cache, and the CPU baseline (the torch fp32 oracle on this host's
-cores, on a bounded sample).
+Infinity Cache, the same encoder with int8 GEMMs (`int8`: the reference's
+per-token / per-channel quantised matmul; an extra line, not `value`), and
+the CPU baseline (the torch fp32 oracle on this host's cores, on a bounded
+sample).
 
 Prints ONE JSON line.
 """
@@ -31,6 +33,7 @@ METRIC = "large-v3 encoder ms @ctx=1500 bs=1; mel-frames/s bs=16; % bf16 MFMA pe
 PEAK_BF16 = 2.5e15      # MI355X dense bf16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12       # MI355X HBM3E, B/s
 PEAK_FP64_TF = 78.6     # MI355X fp64, TFLOP/s
+PEAK_I8 = 5.0e15        # MI355X dense int8 MFMA, OP/s
 # HBM-side bytes per launch of the kernels that can be the dominant stage,
 # measured with `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over
 # whisper-xdna_amd/wxhip/probe.py at the batch-16 shape, each counter scaled
@@ -209,6 +212,36 @@ def cpu_baseline(W, n_mels):
             "ms_per_forward": round(t * 1e3, 1)}
 
 
+def int8_line(enc, mel, args, B, T):
+    """The same encoder with the int8 GEMM path (per-token activation and
+    per-output-channel weight scales, the reference's quantised matmul of
+    bench/probe_int8_decode.py:48-74; attention stays bf16): forward time,
+    batch-1 latency, per-stage times and the int8 MFMA rate of the GEMMs
+    (against MI355X's dense int8 peak, 5.0 POP/s). The out_proj and fc2
+    stages include the quantisation of their A operand (the fp32 attention
+    output, the fp32 GELU(fc1)); LayerNorm quantises its own output."""
+    import numpy as np
+    import torch
+    from wxhip import synth
+    enc.set_int8(True)
+    dt, out = time_forward(enc, mel, args.steps, args.warmup)
+    assert torch.isfinite(out).all().item()
+    profs = [enc.profile(mel) for _ in range(3)]
+    stages = {k: float(np.mean([p[k] for p in profs])) for k in profs[0]}
+    flops = stage_flops(LARGE, B, T)
+    r = {"ms_per_step": round(dt * 1e3, 3), "value": round(B * T / dt, 1),
+         "unit": "mel-frames/s", "stages_ms": {k: round(v, 3) for k, v in stages.items()}}
+    for k in ("qkv", "out_proj", "fc1", "fc2"):
+        if stages.get(k, 0) > 0:
+            r[f"{k}_tops"] = round(flops[k] / (stages[k] / 1e3) / 1e12, 1)
+            r[f"{k}_i8_frac"] = round(flops[k] / (stages[k] / 1e3) / PEAK_I8, 4)
+    if not args.no_latency and T == 3000:
+        dt1, _ = time_forward(enc, mel[:1].contiguous(), max(args.steps, 10), args.warmup)
+        r["latency_bs1_ms"] = round(dt1 * 1e3, 3)
+    enc.set_int8(False)
+    return r
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -218,6 +251,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-rowops", action="store_true")
     ap.add_argument("--no-latency", action="store_true")
+    ap.add_argument("--no-int8", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -237,7 +271,10 @@ def main():
     W = synth.make_weights("large-v3")
     log(f"  {time.perf_counter() - t0:.1f} s")
     dev = wxhip.Device(0)
-    enc = wxhip.HipEncoder(dev, W)
+    # int8 copies of the GEMM weights are made during the upload, for the
+    # int8 line below; the measured forward is the bf16 path
+    enc = wxhip.HipEncoder(dev, W, int8=not args.no_int8)
+    enc.set_int8(False)
     log("weights uploaded")
     mel = torch.from_numpy(synth.make_mel_batch(B, 128, T)).to(dev.device)
 
@@ -302,6 +339,10 @@ def main():
         log(f"l1 latency: {dt1 * 1e3:.2f} ms")
     elif args.workload == "l1":
         res["latency_bs1_ms"] = round(dt * 1e3, 3)
+
+    if not args.no_int8:
+        res["int8"] = int8_line(enc, mel, args, B, T)
+        log(f"int8: {res['int8']}")
 
     res["frontend"] = frontend_rate(dev, B, 128)
     log(f"frontend: {res['frontend']}")
