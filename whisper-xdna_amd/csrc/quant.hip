@@ -36,6 +36,11 @@ __device__ __forceinline__ float row_scale(float m) {
   return s == 0.f ? 1.0f : s;
 }
 
+// Rows are read once: the loads carry the non-temporal hint (cache-policy
+// bit 1), which keeps large activations (fc2's 491 MB fp32 A at batch 16)
+// from displacing what the next GEMM reads.
+constexpr int kCpolNt = 2;
+
 template <int NCH, bool XF32>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const void* __restrict__ xp, int64_t ldx, int rows, int cols, int8_t* __restrict__ q,
@@ -53,15 +58,15 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   for (int c = 0; c < NCH; ++c) {
     const int off = (lane + c * 64) * 8 * esz;
     if (XF32) {
-      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 0);
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kCpolNt);
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, kCpolNt);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         v[c][j] = __uint_as_float(a[j]);
         v[c][j + 4] = __uint_as_float(b[j]);
       }
     } else {
-      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kCpolNt);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         v[c][2 * j] = __uint_as_float(w[j] << 16);
