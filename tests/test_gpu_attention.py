@@ -91,6 +91,34 @@ def test_attention_large_logits_masked_tail(dev):
     assert np.isfinite(got).all() and cosine(got, ref) >= 0.9999
 
 
+@pytest.mark.parametrize("mode", ["", "nosplit"])
+def test_attention_late_max_and_negative_scores(dev, mode, monkeypatch):
+    """The running exp2 reference has to move on a late key block (the last
+    50 keys score ~2^30 above the first block's maximum, so that block's
+    exps overflow the fast path and are redone), and has to settle far below
+    zero when every score is about -80 (identical keys: O = column mean of V).
+    Both against the fp64 closed form."""
+    case(f"attention late max / negative scores {mode}")
+    if mode == "nosplit":
+        monkeypatch.setenv("WXH_ATTN_NOSPLIT", "1")
+    B, T, nh = 1, 1500, 2
+    d = nh * 64
+    rng = np.random.default_rng(8)
+    q = OB.rb((np.abs(rng.normal(0, 1, (B, T, d))) + 0.5).astype(np.float32))
+    k = OB.rb(rng.normal(0, 0.1, (B, T, d)).astype(np.float32))
+    k[:, T - 50:] = OB.rb(2.0 + rng.normal(0, 0.1, (B, 50, d)).astype(np.float32))
+    v = OB.rb(rng.normal(0, 1, (B, T, d)).astype(np.float32))
+    got = _run(dev, q, k, v, nh, 0.125)
+    ref = _ref(q, k, v, nh, 0.125)
+    assert np.isfinite(got).all()
+    assert cosine(got, ref) >= 0.99995, cosine(got, ref)
+    assert np.abs(got - ref).max() <= 2e-2 * np.abs(v).max()
+    kneg = np.full_like(k, -8.0)
+    got = _run(dev, q, kneg, v, nh, 0.125)
+    want = v.astype(np.float64).mean(1, keepdims=True)
+    assert np.isfinite(got).all() and np.abs(got - want).max() < 4e-3
+
+
 def test_attention_bf16_out_and_batch_independence(dev):
     """Batch item b of a batched call equals the same item run alone, bit for bit."""
     case("attention batch independence")

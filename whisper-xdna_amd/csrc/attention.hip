@@ -62,7 +62,7 @@ __device__ __forceinline__ float max_halves(float x) {
 // first half of the key blocks and the other 4 the second half, for the same
 // 4 x 32 queries, each half through its own ring; the halves' (O, max, sum)
 // are combined through LDS at the end.
-template <bool OUT_F32, int KSPLIT>
+template <bool OUT_F32, int KSPLIT, bool QPRE>
 __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ Vt, int n_head, int T, int Tp,
@@ -135,7 +135,12 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
   for (int db = 0; db < 2; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  // mc: the running exp2 reference (log2 domain), set by the first block;
+  // l_run: this lane's share of the row sum
+  float mc = 0.f, l_run = 0.f;
+  f32x16 negm, zero16;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) negm[r] = zero16[r] = 0.f;
   const int sw = (l32 >> 1) & 7;  // the swizzle of every row this lane reads
 
 #pragma unroll
@@ -175,20 +180,30 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
       for (int db = 0; db < 2; ++db)
         va[ks][db] = *reinterpret_cast<const bf16x8*>(
             Vs + (db * 32 + l32) * 128 + (((ks * 2 + half) ^ sw) << 4));
-    // S^T = K Q^T for two 32-key blocks
+    // S^T = K Q^T for two 32-key blocks. Every score leaves this section as
+    // its exp2 argument a = s c - mc, with c = scale * log2(e) and mc the
+    // lane's running reference (log2 domain): with a pre-scaled Q (QPRE) the
+    // accumulators start from -mc (the negm block), so the MFMAs produce a
+    // directly; otherwise they start from zero and one FMA per score forms it.
     f32x16 s[2];
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
+      if constexpr (QPRE)
+        s[k2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[k2][0], qf[0], negm, 0, 0, 0);
+      else
+        s[k2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[k2][0], qf[0], zero16, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[k2][r] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
+      for (int kk = 1; kk < 4; ++kk)
         s[k2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[k2][kk], qf[kk], s[k2], 0, 0, 0);
     }
+    if constexpr (!QPRE) {
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[k2][r] = fmaf(s[k2][r], scale_log2, -mc);
+    }
     // Keys >= T exist only in the last block: mask them there (a uniform
-    // branch), nowhere else. The running max is kept in raw score units and
-    // the scale enters once, in the FMA that forms the exp2 argument:
-    // p = 2^(s c - m c) with c = scale * log2(e), m the running max.
+    // branch), nowhere else.
     if ((kb + 1) * kKB > T) {
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2)
@@ -198,43 +213,60 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
           if (key >= T) s[k2][r] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
+    // p = 2^(a - sub) in bf16 pairs; the block's row sum lb adds exactly
+    // those bf16 values (one v_dot2_f32_bf16 per pair), the same P that
+    // multiplies V
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    uint32_t pk[2][8];
+    float lb;
+    auto exps = [&](auto sub_c, float sub) {
+      constexpr bool SUB = decltype(sub_c)::value;
+      lb = 0.f;
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2)
+      for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[k2][r]);
-    mx = max_halves(mx);
-    // Lazy rescaling: the exponent reference m_run only moves (and O, l are
-    // rescaled by 2^((m_old - m_new) c)) when some lane's max has grown by
-    // more than 8 in the log2 domain; otherwise p = 2^(s c - m_run c) stays
-    // below 2^8, which bf16 P and the fp32 sums hold without loss. The
-    // branch is wave-uniform and, after the first block, rarely taken.
-    const bool grow = (mx - m_run) * scale_log2 > 8.0f;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+        for (int j = 0; j < 8; ++j) {
+          const float a0 = SUB ? s[k2][2 * j] - sub : s[k2][2 * j];
+          const float a1 = SUB ? s[k2][2 * j + 1] - sub : s[k2][2 * j + 1];
+          pk[k2][j] = f2bf2(__builtin_amdgcn_exp2f(a0), __builtin_amdgcn_exp2f(a1));
+          lb = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk[k2][j]), ones, lb,
+                                               false);
+        }
+    };
+    // No block maximum on the common path: the reference mc moves only when
+    // some p of the block exceeds 2^16 (then the block's sum does, too; an
+    // overflow to inf as well), which bf16 P and the fp32 sums hold without
+    // loss. Then -- and on a part's first block, which sets mc from its own
+    // maximum -- the block maximum is taken, mc raised by delta, O and l
+    // rescaled by 2^-delta and the block's exps redone. mc is always an
+    // observed maximum, so the largest score so far contributes p = 1 and l
+    // never underflows. The branch is wave-uniform and after the first block
+    // rarely taken.
+    exps(std::false_type{}, 0.f);
+    if (i == 0 || __builtin_amdgcn_ballot_w64(lb > 65536.0f) != 0) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[k2][r]);
+      mx = max_halves(mx);
+      // first block: O and l are zero, mc takes the block maximum (it may
+      // fall); later: mc only rises
+      const float delta = i == 0 ? mx : fmaxf(mx, 0.f);
+      const float alpha = i == 0 ? 1.f : __builtin_amdgcn_exp2f(-delta);
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-      m_run = m_new;
-    }
-    const float mc = m_run * scale_log2;
-    // P in bf16 pairs; the row sum adds exactly those bf16 values (one
-    // v_dot2_f32_bf16 per pair), the same P that multiplies V
-    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-    uint32_t pk[2][8];
+      mc += delta;
+      if constexpr (QPRE) {
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[k2][2 * j], scale_log2, -mc));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[k2][2 * j + 1], scale_log2, -mc));
-        pk[k2][j] = f2bf2(p0, p1);
-        l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk[k2][j]), ones,
-                                                l_run, false);
+        for (int r = 0; r < 16; ++r) negm[r] = -mc;
       }
+      exps(std::true_type{}, delta);
+    }
+    l_run += lb;
 
     // O^T += V^T P^T, 16 keys per MFMA; Vt rows hold each lane half's 8 keys
     // contiguously (vt_key), so one 16-byte read is the whole A fragment
@@ -282,15 +314,17 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
       for (int db = 0; db < 2; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) xs[(db * 16 + r) * 64] = o[db][r];
-      xs[32 * 64] = m_run;
+      xs[32 * 64] = mc;
       xs[33 * 64] = l_run;
     }
     __syncthreads();
     if (kh == 1) return;
+    // a second part without key blocks (T <= 64) left l = 0, O = 0
     const float m1 = xs[32 * 64], l1 = xs[33 * 64];
-    const float mm = fmaxf(m_run, m1);
-    const float a0 = __builtin_amdgcn_exp2f((m_run - mm) * scale_log2);
-    const float a1 = __builtin_amdgcn_exp2f((m1 - mm) * scale_log2);
+    const bool has1 = !(l1 == 0.f);
+    const float mm = has1 ? fmaxf(mc, m1) : mc;
+    const float a0 = __builtin_amdgcn_exp2f(mc - mm);
+    const float a1 = has1 ? __builtin_amdgcn_exp2f(m1 - mm) : 0.f;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -322,24 +356,24 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
 hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
                             const uint16_t* Vt, int batch, int n_head, int T,
                             float scale, void* O, int o_dtype, int64_t ldo,
-                            hipStream_t s) {
+                            hipStream_t s, bool q_prescaled) {
   if (T <= 0 || batch <= 0 || n_head <= 0) return hipSuccess;
   const int Tp = attn_padded_len(T);
   dim3 grid((T + kQB - 1) / kQB, n_head, batch);
-  const float scale_log2 = scale * 1.4426950408889634f;
+  const float scale_log2 = attn_q_scale(scale);
   // Fewer workgroups than CUs (batch 1: 20 heads x 12 query blocks): split
   // every workgroup's keys over twice the waves, halving each wave's walk.
-  if ((int64_t)grid.x * grid.y * grid.z < 256 && getenv("WXH_ATTN_NOSPLIT") == nullptr) {
-    if (o_dtype == DT_F32)
-      attn_kernel<true, 2><<<grid, 512, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
-    else
-      attn_kernel<false, 2><<<grid, 512, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
-    return hipGetLastError();
-  }
-  if (o_dtype == DT_F32)
-    attn_kernel<true, 1><<<grid, 256, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
-  else
-    attn_kernel<false, 1><<<grid, 256, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, O, ldo);
+  const bool split =
+      (int64_t)grid.x * grid.y * grid.z < 256 && getenv("WXH_ATTN_NOSPLIT") == nullptr;
+  const bool f32 = o_dtype == DT_F32;
+#define WX_ATTN(F32, KS, QP)                                                            \
+  if (f32 == F32 && (KS == 2) == split && q_prescaled == QP)                           \
+    attn_kernel<F32, KS, QP><<<grid, 256 * KS, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, \
+                                                       O, ldo);
+  WX_ATTN(true, 2, true) WX_ATTN(false, 2, true) WX_ATTN(true, 1, true) WX_ATTN(false, 1, true)
+  WX_ATTN(true, 2, false) WX_ATTN(false, 2, false) WX_ATTN(true, 1, false)
+  WX_ATTN(false, 1, false)
+#undef WX_ATTN
   return hipGetLastError();
 }
 

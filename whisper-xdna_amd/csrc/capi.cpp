@@ -723,11 +723,12 @@ int run_body_i8(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer
       e.t_pad = tp;
       e.d_model = d;
       e.rows_per_batch = ctx;
+      e.q_scale = wx::attn_q_scale(scale);
       if (int r = gemm(M, 3 * d, d, W.wqkv_q, W.sqkv, wx::EPI_QKV, e)) return r;
       if (int r = mark(ST_QKV)) return r;
     }
     WXH_HIP(wx::launch_attention(E->q, E->k, E->vt, batch, nh, ctx, scale, E->f32ws,
-                                 wx::DT_F32, d, s));
+                                 wx::DT_F32, d, s, true));
     if (int r = mark(ST_ATTN)) return r;
     {
       WXH_HIP(wx::launch_quantize_rows(E->f32ws, wx::DT_F32, d, M, d, E->aq, d, d, E->asc,
@@ -822,11 +823,12 @@ int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* t
       e.t_pad = tp;
       e.d_model = d;
       e.rows_per_batch = ctx;
+      e.q_scale = wx::attn_q_scale(scale);
       WXH_HIP(wx::launch_gemm(M, 3 * d, d, a, W.wqkv, d, wx::EPI_QKV, e, s));
       if (int r = mark(ST_QKV)) return r;
     }
     WXH_HIP(wx::launch_attention(E->q, E->k, E->vt, batch, nh, ctx, scale, E->o,
-                                 wx::DT_BF16, d, s));
+                                 wx::DT_BF16, d, s, true));
     if (int r = mark(ST_ATTN)) return r;
     {
       wx::GemmA a{E->o, d, M, 0};

@@ -136,7 +136,7 @@ __device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&ac
             static_cast<float*>(e.out)[r0[r] + cofs[j]] =
                 gelu_erf(x) + e.aux[(int64_t)tt[r] * N + cofs[j]];
           } else {  // EPI_QKV
-            const uint16_t val = f2bf(x);
+            const uint16_t val = f2bf(which[j] == 0 ? x * e.q_scale : x);
             if (which[j] == 0)
               e.q[r0[r] + cofs[j]] = val;
             else if (which[j] == 1)
@@ -288,7 +288,8 @@ __device__ __forceinline__ void store_tile_t_impl(const EpiParams& e, const f32x
           const int h = c >> 6, dd = c & 63;
           if (wh < 2) {
             uint16_t* p = (wh == 0 ? e.q : e.k) + r0 + (int64_t)h * e.t_pad * 64 + dd;
-            const u32x2 v = {f2bf2(x[0], x[1]), f2bf2(x[2], x[3])};
+            const float sc = wh == 0 ? e.q_scale : 1.f;
+            const u32x2 v = {f2bf2(x[0] * sc, x[1] * sc), f2bf2(x[2] * sc, x[3] * sc)};
             *reinterpret_cast<u32x2*>(p) = v;
           } else {
             uint16_t* p = e.vt + r1 + ((int64_t)h * 64 + dd) * e.t_pad;
@@ -610,11 +611,12 @@ __device__ __forceinline__ void sk_reduce(__amdgpu_buffer_rsrc_t ws, int64_t sli
 // make the epilogue VALU-bound (GELU) gain nothing here: the direct path
 // already hides its stores under the arithmetic.
 
-// bias + bf16 RNE of the wave's tile into LDS rows [wm * WTM, + WTM)
+// (acc + bias) * mul, bf16 RNE, of the wave's tile into LDS rows
+// [wm * WTM, + WTM)
 template <class C>
 __device__ __forceinline__ void stage_bf16(const f32x16 (&acc)[C::TM][C::TN],
                                            const f32x4 (&bv)[C::TN][4], uint8_t* smem, int wm,
-                                           int wn, int lane) {
+                                           int wn, int lane, float mul) {
   constexpr int ROWB = C::BN * 2, CPR = ROWB / 16;
   static_assert(C::BM * ROWB <= C::S * C::STAGE, "staged tile fits the ring");
   const int l32 = lane & 31, half = lane >> 5;
@@ -624,8 +626,10 @@ __device__ __forceinline__ void stage_bf16(const f32x16 (&acc)[C::TM][C::TN],
     static_for<C::TN>([&](auto j) {
       static_for<4>([&](auto g) {
         const int q = (wn * C::WTN + j * 32 + g * 8) / 8;
-        const f32x4 x = {acc[i][j][g * 4] + bv[j][g][0], acc[i][j][g * 4 + 1] + bv[j][g][1],
-                         acc[i][j][g * 4 + 2] + bv[j][g][2], acc[i][j][g * 4 + 3] + bv[j][g][3]};
+        const f32x4 x = {(acc[i][j][g * 4] + bv[j][g][0]) * mul,
+                         (acc[i][j][g * 4 + 1] + bv[j][g][1]) * mul,
+                         (acc[i][j][g * 4 + 2] + bv[j][g][2]) * mul,
+                         (acc[i][j][g * 4 + 3] + bv[j][g][3]) * mul};
         const u32x2 v = {f2bf2(x[0], x[1]), f2bf2(x[2], x[3])};
         *reinterpret_cast<u32x2*>(rowp + ((q ^ (r % CPR)) << 4)) = v;
       });
@@ -639,7 +643,7 @@ __device__ __forceinline__ void epi_lds_bf16(const EpiParams& e, const f32x16 (&
                                              const f32x4 (&bv)[C::TN][4], uint8_t* smem,
                                              int bm0, int bn0, int wm, int wn, int lane, int tid) {
   constexpr int ROWB = C::BN * 2, CPR = ROWB / 16;
-  stage_bf16<C>(acc, bv, smem, wm, wn, lane);
+  stage_bf16<C>(acc, bv, smem, wm, wn, lane, 1.f);
   __syncthreads();
   constexpr int PER = C::BM * CPR / C::NT;
   static_assert(PER * C::NT == C::BM * CPR, "whole chunks per thread");
@@ -661,9 +665,9 @@ __device__ __forceinline__ void epi_lds_qk(const EpiParams& e, const f32x16 (&ac
                                            const f32x4 (&bv)[C::TN][4], uint8_t* smem, int bm0,
                                            int bn0, int wm, int wn, int lane, int tid) {
   constexpr int ROWB = C::BN * 2, CPR = ROWB / 16;
-  stage_bf16<C>(acc, bv, smem, wm, wn, lane);
-  __syncthreads();
   const int wh = bn0 / e.d_model;
+  stage_bf16<C>(acc, bv, smem, wm, wn, lane, wh == 0 ? e.q_scale : 1.f);
+  __syncthreads();
   const int h0 = (bn0 - wh * e.d_model) >> 6;
   uint16_t* base = wh == 0 ? e.q : e.k;
   const int T = e.rows_per_batch;

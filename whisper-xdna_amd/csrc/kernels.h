@@ -88,6 +88,9 @@ struct EpiParams {
   int n_head = 0;
   int t_pad = 0;                   // padded key length of Q/K/Vt
   int d_model = 0;
+  // EPI_QKV: the Q part is written as bf16((acc + bias) * q_scale), so the
+  // attention kernel can take Q pre-multiplied by its softmax scale
+  float q_scale = 1.f;
   // Split-K workspace (optional). With it, launch_gemm may split K over
   // `splits` workgroups per output tile when there are too few tiles to fill
   // the GPU: each writes its fp32 partial to sk_ws ([splits][M][N]), and the
@@ -155,11 +158,17 @@ __host__ __device__ inline int vt_key(int t) {
 
 // Q, K: [B*nh, Tp, 64] bf16; Vt: [B*nh, 64, Tp] bf16 with keys placed by
 // vt_key (Tp = padded T, pads finite). O row (b*T + t), column h*64 + j;
-// bf16 or fp32 per o_dtype.
+// bf16 or fp32 per o_dtype. With q_prescaled, Q already holds
+// bf16(q * scale * log2(e)) (attn_q_scale), written so by the QKV GEMM's
+// epilogue, and `scale` is not used.
 hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
                             const uint16_t* Vt, int batch, int n_head, int T,
                             float scale, void* O, int o_dtype, int64_t ldo,
-                            hipStream_t s);
+                            hipStream_t s, bool q_prescaled = false);
+
+// The factor a pre-scaled Q carries: the softmax scale times log2(e), so
+// that a score leaves the MFMA in the exp2 domain.
+inline float attn_q_scale(float scale) { return scale * 1.4426950408889634f; }
 
 // fp32 q, k, v rows [B*T, nh*64] (ld ld) -> the attention operand layouts.
 hipError_t launch_pack_qkv(const float* q, const float* k, const float* v,
