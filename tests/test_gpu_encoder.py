@@ -114,6 +114,27 @@ def test_large_v3_encoder_cosine(dev, large):
     assert c >= 0.994
 
 
+def test_large_v3_batch16_bench_workload(dev, large):
+    """The benchmark's own workload: large-v3 (32 layers, ctx 1500) on the
+    batch of 16 mels of seeds 0..15, one graph replay, where every GEMM runs
+    the batch-16 tiles (256x256). Items 0 and 15 against the oracle (the
+    large-v3 gate); every item against the same mel run alone at batch 1
+    (128x128 tiles, split-K fc2 and conv2: the same arithmetic up to fp32
+    summation order, so far closer to each other than to the oracle)."""
+    case("encoder large-v3 32 layers batch 16 (bench workload)")
+    mels = synth.make_mel_batch(16, 128, 3000)
+    enc = _enc(dev, large)
+    got = _fwd(enc, mels, dev)
+    assert got.shape == (16, 1500, 1280) and np.isfinite(got).all()
+    one = np.stack([_fwd(enc, mels[b], dev) for b in range(16)])
+    c_items = [cosine(got[b], one[b]) for b in range(16)]
+    c_ref = [cosine(got[b], OE.encoder_torch(large, mels[b])) for b in (0, 15)]
+    report("large_v3_batch16", cosine_batched_vs_single_min=min(c_items),
+           cosine_vs_oracle=c_ref)
+    assert min(c_ref) >= 0.994, c_ref
+    assert min(c_items) >= 0.999, c_items
+
+
 def test_split_k_batch1(dev, large, monkeypatch):
     """At batch 1 the large-v3 fc2 (K 5120) and conv2 (K 3840) GEMMs have
     120 output tiles of 128x128 and split K over two workgroups per tile.
