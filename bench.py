@@ -82,16 +82,26 @@ def stage_launches(g):
             "fc1": nl, "fc2": nl, "layernorm": 2 * nl, "ln_post": 1, "prep": 1}
 
 
-def time_forward(enc, mel, steps, warmup):
+def time_forward(enc, mel, steps, warmup, host=None):
+    """Wall time per forward over `steps` graph replays (synchronised on
+    both sides). With `host` (a dict), also the host CPU time (user + system
+    of every thread of the process, the quantity bench/run_raw_encoder.py:
+    113-118 reports from os.times, here from time.process_time for its finer
+    resolution) that issuing them took, per forward: the host's whole share
+    of the forward, since the replays run on the GPU."""
     import torch
     for _ in range(warmup):
         enc.forward(mel)
     torch.cuda.synchronize()
+    c0 = time.process_time()
     t0 = time.perf_counter()
     for _ in range(steps):
         out = enc.forward(mel)
+    c1 = time.process_time()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / steps
+    if host is not None:
+        host["host_cpu_ms_per_step"] = round((c1 - c0) / steps * 1e3, 3)
     return dt, out
 
 
@@ -299,7 +309,8 @@ def main():
     log("weights uploaded")
     mel = torch.from_numpy(synth.make_mel_batch(B, 128, T)).to(dev.device)
 
-    dt, out = time_forward(enc, mel, args.steps, args.warmup)
+    host = {}
+    dt, out = time_forward(enc, mel, args.steps, args.warmup, host)
     assert torch.isfinite(out).all().item()
     frames = B * T
     log(f"{args.workload}: {dt * 1e3:.2f} ms/forward, {frames / dt:.0f} mel-frames/s")
@@ -348,6 +359,7 @@ def main():
                      "flop_per_launch": flop_per_launch,
                      "avg_launch_us": round(per_launch_s * 1e6, 2)},
         "stages": kern,
+        **host,
     }
 
     if not args.no_latency and args.workload != "l1":
