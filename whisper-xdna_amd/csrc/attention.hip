@@ -10,8 +10,11 @@
 // ever reaches HBM.
 //
 // The reference scales q and k by hd^-1/4 each (npu_whisper_encoder.py:461);
-// here the product scale^2 = 1/sqrt(hd) is applied once to the fp32 scores,
-// which is the same function with one rounding less.
+// here the product scale^2 = 1/sqrt(hd), times log2(e), is applied once: in
+// the encoder by the QKV GEMM's epilogue, to q in fp32 before its bf16
+// rounding (QPRE: the kernel then reads scores in the exp2 domain straight
+// from the MFMAs), and for the C ABI's raw Q to the fp32 scores. Either way
+// it is the same function with one rounding less.
 //
 // Layout: Q, K [B*nh, Tp, 64] and Vt [B*nh, 64, Tp] bf16 (Tp = T rounded up
 // to 64, pad rows/columns finite; Vt keys placed by vt_key). A workgroup owns
