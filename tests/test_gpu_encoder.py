@@ -120,12 +120,15 @@ def test_large_v3_batch16_bench_workload(dev, large):
     the batch-16 tiles (256x256). Items 0 and 15 against the oracle (the
     large-v3 gate); every item against the same mel run alone at batch 1
     (128x128 tiles, split-K fc2 and conv2: the same arithmetic up to fp32
-    summation order, so far closer to each other than to the oracle)."""
+    summation order, so far closer to each other than to the oracle); a
+    second replay bit for bit."""
     case("encoder large-v3 32 layers batch 16 (bench workload)")
     mels = synth.make_mel_batch(16, 128, 3000)
     enc = _enc(dev, large)
     got = _fwd(enc, mels, dev)
     assert got.shape == (16, 1500, 1280) and np.isfinite(got).all()
+    # a second replay of the captured graph is bit-identical
+    np.testing.assert_array_equal(_fwd(enc, mels, dev), got)
     one = np.stack([_fwd(enc, mels[b], dev) for b in range(16)])
     c_items = [cosine(got[b], one[b]) for b in range(16)]
     c_ref = [cosine(got[b], OE.encoder_torch(large, mels[b])) for b in (0, 15)]
