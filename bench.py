@@ -286,7 +286,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the encoder shards as independent batch items; see DESIGN.md)",
+              "(the encoder would shard as independent batch items, one group per GPU "
+              "with replicated weights and no collective; that is not built)",
               file=sys.stderr)
         sys.exit(2)
 
