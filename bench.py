@@ -285,7 +285,7 @@ def main():
     ap.add_argument("--no-int8", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: there is no multi-GPU path "
               "(the encoder would shard as independent batch items, one group per GPU "
               "with replicated weights and no collective; that is not built)",
               file=sys.stderr)

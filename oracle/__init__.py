@@ -2,8 +2,9 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the product package (``wxhip``) imports
 this package; only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may use it, and there only as the checker
-(or as the timed CPU baseline), never as something a product path calls.
+``cpu_baseline`` leg of ``bench.py`` may use it, and there only as the
+reference answer a result is compared with (or as the timed CPU baseline),
+never as something a product path calls.
 
 Modules
 -------

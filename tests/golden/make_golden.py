@@ -10,7 +10,7 @@ encoder_tiny_2layer_ctx50.npz tiny-shaped 2-layer encoder, seed-0 weights,
                               mel [80, 100] from seed 0, through the torch
                               fp32 oracle
 
-The fixtures are produced by this build's own oracle (the reference's Python
+The fixtures are produced by the oracle in oracle/ (the reference's Python
 is not run), so they pin the oracle against regressions and give the GPU tests
 a CPU-free expected answer.
 """

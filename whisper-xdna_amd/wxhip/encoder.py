@@ -3,7 +3,7 @@
 ``encoder(W, mel, mm, attn_mm, n_layer=4, n_head=6, prof=None, fused_gelu=False,
 npu_softmax=False, attn_fn=None, mlp_fn=None, fold_bias=True)`` keeps the
 signature of npu_whisper_encoder.py:436-541. The plugs must be a HipRT's
-(``rt.matmul``, ``rt.attn_chain``, ``rt.mlp``) -- this build has no CPU
+(``rt.matmul``, ``rt.attn_chain``, ``rt.mlp``) -- there is no CPU
 backend, so a plug from anywhere else raises TypeError. Two device paths:
 
 * the whole forward as one hipGraph over device-resident weights
@@ -158,8 +158,8 @@ def _runtime_of(fn):
     if not isinstance(rt, HipRT):
         rt = getattr(fn, "rt", None)
     if not isinstance(rt, HipRT):
-        raise TypeError("encoder(): mm must be a HipRT's matmul (this build runs the "
-                        "encoder on the GPU only; there is no numpy backend)")
+        raise TypeError("encoder(): mm must be a HipRT's matmul (the encoder runs "
+                        "on the GPU only; there is no numpy backend)")
     return rt
 
 
