@@ -211,6 +211,36 @@ def frontend_rate(dev, batch, n_mels):
             "fp64_frac": round(flop / us / 1e6 / PEAK_FP64_TF, 4)}
 
 
+def cpu_rowops():
+    """The oracle's row ops on the host, on the standalone rowops shapes
+    (numpy, one core): LayerNorm [1500, 1280] and softmax [30000, 1500] in
+    float64, erf-GELU [1500, 5120] as the reference's own fp32 A&S 7.1.26
+    evaluation (npu_whisper_encoder.py:284-300). Median of 3; the softmax is
+    timed once on its first 3000 rows (a tenth of the shape, about half a
+    second), so its "ms" is for that sample. GB/s over the same algorithmic
+    bytes as the GPU row-kernel figures (bf16 in and out)."""
+    import numpy as np
+    from oracle import rowops as OR
+    from wxhip import synth
+    x = synth.rowop_inputs(seed=0)
+    cases = [("layernorm_1500x1280", lambda: OR.layer_norm(x["ln_x"], x["ln_gamma"], x["ln_beta"]),
+              x["ln_x"].size, 3),
+             ("gelu_erf_1500x5120", lambda: OR.gelu_erf_as_f32(x["gelu_x"]), x["gelu_x"].size, 3),
+             ("softmax_30000x1500", lambda: OR.softmax(x["sm_x"][:3000]), 3000 * 1500, 1)]
+    out = {}
+    for name, fn, n, reps in cases:
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        t = float(np.median(ts))
+        out[name] = {"ms": round(t * 1e3, 2), "GB/s": round(4 * n / t / 1e9, 2)}
+    out["cores"] = 1
+    out["sample"] = "softmax: rows 0..2999 of [30000, 1500]; the others whole"
+    return out
+
+
 def cpu_baseline(W, n_mels):
     """torch fp32 oracle on this host's cores: one warmup and two timed
     forwards of one large-v3 sample (3000 mel frames)."""
@@ -237,6 +267,7 @@ def cpu_baseline(W, n_mels):
     fe_ms = (time.perf_counter() - t0) / 3 * 1e3
     return {"value": round(3000 / t, 1), "unit": "mel-frames/s",
             "frontend_log_mel_ms_per_clip": round(fe_ms, 2),
+            "rowops": cpu_rowops(),
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": "1 of the 16 large-v3 mels (3000 frames, batch 1), torch fp32 "
                       "encoder restatement, median of 2 after 1 warmup",
