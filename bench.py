@@ -243,14 +243,16 @@ def cpu_rowops():
 
 def cpu_baseline(W, n_mels):
     """torch fp32 oracle on this host's cores: one warmup and two timed
-    forwards of one large-v3 sample (3000 mel frames)."""
+    forwards of one large-v3 sample (3000 mel frames, seed 0: item 0 of the
+    measured batch). Returns the figures and the oracle's features for that
+    sample."""
     import numpy as np
     import torch
     from oracle import encoder as OE
     from wxhip import synth
     torch.set_num_threads(min(os.cpu_count() or 1, 16))
     mel = synth.make_mel(n_mels, 3000, seed=0)
-    OE.encoder_torch(W, mel)
+    ref = OE.encoder_torch(W, mel)
     ts = []
     for _ in range(2):
         t0 = time.perf_counter()
@@ -271,7 +273,7 @@ def cpu_baseline(W, n_mels):
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": "1 of the 16 large-v3 mels (3000 frames, batch 1), torch fp32 "
                       "encoder restatement, median of 2 after 1 warmup",
-            "ms_per_forward": round(t * 1e3, 1)}
+            "ms_per_forward": round(t * 1e3, 1)}, ref
 
 
 def int8_line(enc, mel, args, B, T):
@@ -344,6 +346,7 @@ def main():
     host = {}
     dt, out = time_forward(enc, mel, args.steps, args.warmup, host)
     assert torch.isfinite(out).all().item()
+    out0 = out[0].float().cpu().numpy()  # item 0 of the timed forward
     frames = B * T
     log(f"{args.workload}: {dt * 1e3:.2f} ms/forward, {frames / dt:.0f} mel-frames/s")
 
@@ -422,8 +425,14 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         log("cpu baseline (torch fp32, one large-v3 sample) ...")
-        res["cpu_baseline"] = cpu_baseline(W, 128)
+        res["cpu_baseline"], ref0 = cpu_baseline(W, 128)
         log(f"  {res['cpu_baseline']}")
+        if T == 3000:
+            # parity of the measured run: its item 0 against the oracle
+            a = out0.astype(np.float64).ravel()
+            b = np.asarray(ref0, np.float64).ravel()
+            res["cosine_item0_vs_oracle"] = round(
+                float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b))), 7)
     print(json.dumps(res), flush=True)
 
 
