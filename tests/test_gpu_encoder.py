@@ -138,6 +138,25 @@ def test_large_v3_batch16_bench_workload(dev, large):
     assert min(c_items) >= 0.999, c_items
 
 
+def test_large_v3_batch16_ctx512(dev, large):
+    """The reduced-context batch-16 workload: large-v3 (32 layers) on 16
+    mels of 1024 frames (ctx 512, seeds 0..15). The positional embedding is
+    sliced to 512 as the reference does. Items 0 and 15 against the oracle
+    (the large-v3 gate); every item against the same mel run alone."""
+    case("encoder large-v3 32 layers batch 16 ctx 512")
+    mels = synth.make_mel_batch(16, 128, 1024)
+    enc = _enc(dev, large)
+    got = _fwd(enc, mels, dev)
+    assert got.shape == (16, 512, 1280) and np.isfinite(got).all()
+    one = np.stack([_fwd(enc, mels[b], dev) for b in range(16)])
+    c_items = [cosine(got[b], one[b]) for b in range(16)]
+    c_ref = [cosine(got[b], OE.encoder_torch(large, mels[b])) for b in (0, 15)]
+    report("large_v3_batch16_ctx512", cosine_batched_vs_single_min=min(c_items),
+           cosine_vs_oracle=c_ref)
+    assert min(c_ref) >= 0.994, c_ref
+    assert min(c_items) >= 0.999, c_items
+
+
 def test_split_k_batch1(dev, large, monkeypatch):
     """At batch 1 the large-v3 fc2 (K 5120) and conv2 (K 3840) GEMMs have
     120 output tiles of 128x128 and split K over two workgroups per tile.
