@@ -3,6 +3,7 @@
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
                     [--no-rowops] [--no-int8] [--workload l16|l1|l16s]
+    python bench.py --probe KERNEL [--reps N] [--batch B]   (counter runs)
 
 A step is one encoder forward (mel -> features) of the workload over inputs
 already resident in HBM, replayed as the captured hipGraph. Default workload:
@@ -19,6 +20,17 @@ the CPU baseline (the torch fp32 oracle on this host's cores, on a bounded
 sample).
 
 Prints ONE JSON line.
+
+--probe KERNEL runs one kernel of the large-v3-shaped encoder (batch B,
+default 16) N times on seeded operands through the C ABI, after N plain
+512 MiB device copies, and prints no JSON: it is the program the rocprofv3
+counter runs in profiles/ profile. The copies' FETCH_SIZE / WRITE_SIZE
+against their known byte count give the factor that turns the kernel's
+readings into bytes. KERNEL: fc1 (erf-GELU epilogue, bf16 out), fc2 and
+out_proj (fp32 residual epilogue), qkv (the QKV main loop with a plain bf16
+epilogue), attention (softmax(Q K^T / 8) V over B*20 heads of 1500 keys),
+rowops (LayerNorm [1500,1280] bf16 and [24000,1280] fp32 -> bf16, erf- and
+poly4-GELU [1500,5120], softmax [30000,1500], each N times).
 """
 import argparse
 import json
@@ -37,8 +49,8 @@ PEAK_FP64_TF = 78.6     # MI355X fp64, TFLOP/s
 PEAK_I8 = 5.0e15        # MI355X dense int8 MFMA, OP/s
 # HBM-side bytes per launch of the kernels that can be the dominant stage,
 # measured with `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over
-# whisper-xdna_amd/wxhip/probe.py at the batch-16 shape, each counter scaled
-# by what it reads for a 512 MiB device copy (FETCH_SIZE x 2.000, WRITE_SIZE
+# `bench.py --probe KERNEL` at the batch-16 shape, each counter scaled by
+# what it reads for a 512 MiB device copy (FETCH_SIZE x 2.000, WRITE_SIZE
 # x 1.000); the summaries, with their commands, are in profiles/.
 TRAFFIC_BYTES = {
     "fc1": (1.0687e9, "profiles/gemm_fc1_l16_traffic.md"),
@@ -125,10 +137,78 @@ def latency_median(enc, mel, n, warmup):
     return float(np.median([a.elapsed_time(b) for a, b in evs])) / 1e3
 
 
+PROBE_KERNELS = ("fc1", "fc2", "qkv", "out_proj", "attention", "rowops")
+
+
+def probe(kernel, reps, batch):
+    """One kernel at its large-v3 shape, `reps` times, after `reps` plain
+    512 MiB device copies (the counters' scale reference); see the module
+    doc. Prints a line per phase."""
+    import torch
+    import wxhip
+    from wxhip import _lib as L
+    D, NH, CTX, FF = 1280, 20, 1500, 5120
+    copy_bytes = 512 << 20
+    dev = wxhip.Device(0)
+    g = torch.Generator(device=dev.device).manual_seed(0)
+    M = batch * CTX
+
+    def normal(shape, std, dtype=torch.bfloat16):
+        return (torch.randn(shape, generator=g, device=dev.device) * std).to(dtype)
+
+    src = torch.empty(copy_bytes // 2, dtype=torch.bfloat16, device=dev.device).normal_(generator=g)
+    dst = torch.empty_like(src)
+    if kernel in ("fc1", "fc2", "qkv", "out_proj"):
+        K, N = {"fc1": (D, FF), "fc2": (FF, D), "qkv": (D, 3 * D), "out_proj": (D, D)}[kernel]
+        A, W, b = normal((M, K), 1.0), normal((N, K), 0.02), normal((N,), 0.02, torch.float32)
+        if kernel in ("fc1", "qkv"):
+            # the fused QKV epilogue exists only inside the encoder graph; the
+            # C ABI's bf16 epilogue runs the same main loop over the same shape
+            out = torch.empty(M, N, dtype=torch.bfloat16, device=dev.device)
+            epi = L.WXH_EPI_BF16_GELU_ERF if kernel == "fc1" else L.WXH_EPI_BF16
+            cases = [(kernel, lambda: dev.gemm(A, W, b, epi, out=out))]
+        else:
+            x = normal((M, N), 1.0, torch.float32)
+            cases = [(kernel, lambda: dev.gemm(A, W, b, L.WXH_EPI_RESID_F32, out=x))]
+    elif kernel == "attention":
+        Q, Kt, Vt = dev.attn_buffers(batch, NH, CTX)
+        for t in (Q, Kt, Vt):
+            t.copy_(normal(t.shape, 1.0))
+        cases = [(kernel, lambda: dev.attention(Q, Kt, Vt, batch, NH, CTX, 64 ** -0.5))]
+    else:
+        x = normal((1500, 1280), 2.0)
+        gm = 1 + normal((1280,), 0.1, torch.float32)
+        bt = normal((1280,), 0.1, torch.float32)
+        y = torch.empty_like(x)
+        xf = normal((24000, 1280), 2.0, torch.float32)
+        yf = torch.empty(24000, 1280, dtype=torch.bfloat16, device=dev.device)
+        xg = normal((1500, 5120), 3.0)
+        yg = torch.empty_like(xg)
+        xs = normal((30000, 1500), 4.0)
+        ys = torch.empty_like(xs)
+        cases = [("layernorm 1500x1280 bf16", lambda: dev.layer_norm(x, gm, bt, out=y)),
+                 ("layernorm 24000x1280 f32->bf16", lambda: dev.layer_norm(xf, gm, bt, out=yf)),
+                 ("gelu erf 1500x5120", lambda: dev.gelu(xg, L.WXH_GELU_ERF, out=yg)),
+                 ("gelu poly4 1500x5120", lambda: dev.gelu(xg, L.WXH_GELU_POLY4_RNE, out=yg)),
+                 ("softmax 30000x1500", lambda: dev.softmax_rows(xs, out=ys))]
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[probe] copy {copy_bytes} bytes x {reps}", flush=True)
+    for name, fn in cases:
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        print(f"[probe] {name} (batch {batch}) x {reps}", flush=True)
+
+
 def rowop_bandwidth(dev):
     """Row kernels over rotating buffer sets > 256 MB, captured in a graph so
     launch gaps do not count; returns GB/s per kernel (algorithmic bytes =
-    one read + one write of every element)."""
+    one read + one write of every element). Beside each, `copy_frac`: the
+    kernel's rate over that of a plain device copy (torch's copy or
+    conversion kernel) moving the same bytes per element under the same
+    protocol, the practical ceiling at that size."""
     import torch
     from wxhip import _lib as L
     out = {}
@@ -157,29 +237,37 @@ def rowop_bandwidth(dev):
             else:
                 dev.softmax_rows(xs[i], out=ys[i])
 
-        for i in range(nset):
-            run(i)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        def graphed_seconds(fn):
+            """Seconds per launch of fn(i) over the rotating set, graph-replayed."""
             for i in range(nset):
-                run(i)
-        graph.replay()
-        torch.cuda.synchronize()
-        reps = 5
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
+                fn(i)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(nset):
+                    fn(i)
             graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        per = e0.elapsed_time(e1) / 1e3 / (reps * nset)
+            torch.cuda.synchronize()
+            reps = 5
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / 1e3 / (reps * nset)
+
+        per = graphed_seconds(run)
+        # the same bytes moved by a plain copy (fp32 -> bf16: the conversion)
+        per_copy = graphed_seconds(lambda i: ys[i].copy_(xs[i]))
         nbytes = (xs[0].element_size() + 2) * shape[0] * shape[1]
         gbs = nbytes / per / 1e9
         out[name] = {"us": round(per * 1e6, 2), "GB/s": round(gbs, 1),
                      "hbm_frac": round(gbs * 1e9 / PEAK_HBM, 3),
+                     "copy_us": round(per_copy * 1e6, 2),
+                     "copy_frac": round(per_copy / per, 3),
                      "working_set_MB": round(nset * nbytes / 1e6)}
-        del xs, ys, graph
+        del xs, ys
         torch.cuda.empty_cache()
     return out
 
@@ -242,19 +330,21 @@ def cpu_rowops():
 
 
 def cpu_baseline(W, n_mels):
-    """torch fp32 oracle on this host's cores: one warmup and two timed
+    """torch fp32 oracle on this host's cores: one warmup and three timed
     forwards of one large-v3 sample (3000 mel frames, seed 0: item 0 of the
-    measured batch). Returns the figures and the oracle's features for that
-    sample."""
+    measured batch), with one thread per core this process may run on (its
+    CPU affinity; the host's total core count is reported beside it).
+    Returns the figures and the oracle's features for that sample."""
     import numpy as np
     import torch
     from oracle import encoder as OE
     from wxhip import synth
-    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    torch.set_num_threads(max(1, usable or 1))
     mel = synth.make_mel(n_mels, 3000, seed=0)
     ref = OE.encoder_torch(W, mel)
     ts = []
-    for _ in range(2):
+    for _ in range(3):
         t0 = time.perf_counter()
         OE.encoder_torch(W, mel)
         ts.append(time.perf_counter() - t0)
@@ -270,10 +360,38 @@ def cpu_baseline(W, n_mels):
     return {"value": round(3000 / t, 1), "unit": "mel-frames/s",
             "frontend_log_mel_ms_per_clip": round(fe_ms, 2),
             "rowops": cpu_rowops(),
-            "cores": torch.get_num_threads(), "kind": "port",
+            "cores": torch.get_num_threads(), "host_cores": os.cpu_count(),
+            "affinity_cores": usable, "kind": "port",
             "sample": "1 of the 16 large-v3 mels (3000 frames, batch 1), torch fp32 "
-                      "encoder restatement, median of 2 after 1 warmup",
+                      "encoder restatement, median of 3 after 1 warmup, one thread "
+                      "per core of the process's CPU affinity",
             "ms_per_forward": round(t * 1e3, 1)}, ref
+
+
+def stage_roofline(enc, mel):
+    """Per-stage device times of one workload (mean of 3 un-graphed
+    profile forwards, HIP events on the library stream) and the roofline of
+    its dominant GEMM / attention kernel: algorithmic FLOP per launch over
+    its average launch time, against the bf16 dense peak."""
+    import numpy as np
+    B, _, T = mel.shape
+    profs = [enc.profile(mel) for _ in range(3)]
+    stages = {k: float(np.mean([p[k] for p in profs])) for k in profs[0]}
+    flops = stage_flops(LARGE, B, T)
+    launches = stage_launches(LARGE)
+    per = {}
+    for k, ms in stages.items():
+        e = {"ms": round(ms, 3), "us_per_launch": round(ms * 1e3 / launches[k], 2)}
+        if k in flops and ms > 0:
+            e["mfma_frac"] = round(flops[k] / (ms / 1e3) / PEAK_BF16, 4)
+        per[k] = e
+    dom = max((k for k in flops), key=lambda k: stages[k])
+    s_launch = stages[dom] / 1e3 / launches[dom]
+    f_launch = flops[dom] / launches[dom]
+    return {"bound": "mfma", "kernel": dom, "achieved": round(f_launch / s_launch / 1e12, 1),
+            "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+            "frac": round(f_launch / s_launch / PEAK_BF16, 4), "flop_per_launch": f_launch,
+            "avg_launch_us": round(s_launch * 1e6, 2), "batch": int(B), "stages": per}
 
 
 def int8_line(enc, mel, args, B, T):
@@ -316,6 +434,9 @@ def main():
     ap.add_argument("--no-rowops", action="store_true")
     ap.add_argument("--no-latency", action="store_true")
     ap.add_argument("--no-int8", action="store_true")
+    ap.add_argument("--probe", choices=PROBE_KERNELS, default=None)
+    ap.add_argument("--reps", type=int, default=4)
+    ap.add_argument("--batch", type=int, default=16)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: there is no multi-GPU path "
@@ -323,6 +444,9 @@ def main():
               "with replicated weights and no collective; that is not built)",
               file=sys.stderr)
         sys.exit(2)
+    if args.probe:
+        probe(args.probe, args.reps, args.batch)
+        return
 
     import numpy as np
     import torch
@@ -406,10 +530,12 @@ def main():
         res["latency_bs1_ms_mean_back_to_back"] = round(dt1m * 1e3, 3)
         f1 = sum(stage_flops(LARGE, 1, 3000).values())
         res["latency_bs1_mfma_frac"] = round(f1 / dt1 / PEAK_BF16, 4)
-        log(f"l1 latency: {dt1 * 1e3:.2f} ms")
+        res["roofline_bs1"] = stage_roofline(enc, mel1)
+        log(f"l1 latency: {dt1 * 1e3:.2f} ms; {res['roofline_bs1']}")
     elif args.workload == "l1":
         res["latency_bs1_ms"] = round(latency_median(enc, mel, max(args.steps, 20), 2) * 1e3, 3)
         res["latency_bs1_ms_mean_back_to_back"] = round(dt * 1e3, 3)
+        res["roofline_bs1"] = stage_roofline(enc, mel)
 
     if not args.no_int8:
         res["int8"] = int8_line(enc, mel, args, B, T)

@@ -36,7 +36,8 @@ enum {
   WXH_ERR_HIP = 2,         /* a HIP runtime call failed */
   WXH_ERR_INJECTED = 3,    /* fault injection (wxh_set_fail_inject) */
   WXH_ERR_UNSUPPORTED = 4, /* shape or variant outside what is built */
-  WXH_ERR_STATE = 5        /* e.g. encoder weights incomplete */
+  WXH_ERR_STATE = 5,       /* e.g. encoder weights incomplete */
+  WXH_ERR_TIMEOUT = 6      /* a blocking wait passed the context's deadline */
 };
 
 enum { WXH_BF16 = 0, WXH_F32 = 1, WXH_I8 = 2 };
@@ -93,9 +94,31 @@ int wxh_set_fail_inject(wxh_ctx* ctx, uint32_t mask);
 /* The context's stream (a hipStream_t), e.g. to order caller work after it. */
 int wxh_get_stream(wxh_ctx* ctx, void** stream);
 
-/* Block until all work on the context's stream is done. Replaces the
- * reference's run waits (rawxrt.py:319-324, r.wait(RUN_TIMEOUT_MS)). */
+/* Block until all work on the context's stream is done, or until the
+ * context's deadline (wxh_set_timeout) passes: then WXH_ERR_TIMEOUT. Replaces
+ * the reference's run waits (rawxrt.py:319-324, r.wait(RUN_TIMEOUT_MS)). */
 int wxh_synchronize(wxh_ctx* ctx);
+
+/* Deadline in milliseconds for every blocking wait the library makes on
+ * this context and its encoders (wxh_synchronize, wxh_encoder_forward_host,
+ * wxh_encoder_profile): the wait polls a completion event and gives up with
+ * WXH_ERR_TIMEOUT once the deadline passes. 0 (the default) waits without a
+ * deadline. The device work itself is not cancelled: it runs to completion,
+ * and every buffer it uses stays owned by the library until it has (a
+ * timed-out wxh_encoder_forward_host leaves the caller's output untouched).
+ * The analogue of the reference's NPU_RUN_TIMEOUT_MS deadline, whose expiry
+ * trips the normal fallback (rawxrt.py:51-53, 319-324). */
+int wxh_set_timeout(wxh_ctx* ctx, int timeout_ms);
+
+/* Tuning switches of a context, for tests and measurements (value 0 is the
+ * automatic choice, the default):
+ *  WXH_TUNE_GEMM_SPLITK: split count of the encoder GEMMs with fewer output
+ *    tiles than CUs (1 never splits, n >= 2 splits K n ways where K allows);
+ *  WXH_TUNE_ATTN_KEYSPLIT: 1 never splits a workgroup's keys over two wave
+ *    groups (wxh_attention and the encoder's attention).
+ * Encoders take the context's values when they are created. */
+enum { WXH_TUNE_GEMM_SPLITK = 0, WXH_TUNE_ATTN_KEYSPLIT = 1 };
+int wxh_set_tuning(wxh_ctx* ctx, int what, int value);
 
 /* --------------------------------------------------------------- front end */
 
@@ -241,6 +264,10 @@ typedef struct {
   int n_ctx;    /* positional-embedding rows (1500) */
   int mlp_gelu; /* WXH_GELU_ERF or WXH_GELU_POLY4_RNE (the g4f MLP of
                    RawRT.mlp, rawxrt.py:459-544) */
+  int conv_gelu;/* GELU of both conv layers: WXH_GELU_ERF (the reference's
+                   numpy gelu) or WXH_GELU_POLY4_RNE (its callers' E.gelu =
+                   rt.gelu with GELU_OP g4r, bench/run_raw_encoder.py:82-83,
+                   serve/npu_stt_server.py:203) */
 } wxh_encoder_dims;
 
 /* Create an encoder bound to `ctx`. Weights are device-resident bf16 for the
@@ -267,14 +294,21 @@ int wxh_encoder_ready(wxh_encoder* enc);
  * [batch, ctx, d_model], ctx = (n_frames - 1) / 2 + 1 (<= n_ctx; the
  * positional embedding is sliced to ctx, npu_whisper_encoder.py:456-458).
  * Device pointers; stream-ordered. The body is captured into a hipGraph per
- * (batch, n_frames) on first use and replayed afterwards.
+ * (batch, n_frames) on first use and replayed afterwards. An encoder's
+ * workspace is shared by all its calls: a call on another stream than the
+ * previous one first makes its stream wait for the previous call, and a
+ * call that has to grow the workspace waits for it on the host.
  * Replaces encoder(W, mel, rt.matmul, rt.matmul, attn_fn=rt.attn_chain,
  * mlp_fn=rt.mlp) (npu_whisper_encoder.py:436-541) as driven by
  * bench/run_raw_encoder.py:79-116. */
 int wxh_encoder_forward(wxh_encoder* enc, const float* mel, int batch,
                         int n_frames, float* out, void* stream);
 
-/* Same with host buffers (copies in, runs, copies out; synchronous). */
+/* Same with host buffers: copies in, runs and copies out through staging
+ * buffers the encoder owns (pinned host, device; grown to the largest call),
+ * synchronous under the context's deadline (wxh_set_timeout). On
+ * WXH_ERR_TIMEOUT the caller's buffers are no longer in use and out_host is
+ * untouched; the forward finishes on the device. */
 int wxh_encoder_forward_host(wxh_encoder* enc, const float* mel_host,
                              int batch, int n_frames, float* out_host);
 

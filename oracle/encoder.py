@@ -32,10 +32,33 @@ def geometry(W):
     return n_layer, d // 64
 
 
-def encoder_torch(W, mel, n_layer=None, n_head=None):
-    """mel fp32 [n_mels, T] or [B, n_mels, T] -> fp32 [ctx, d] or [B, ctx, d]."""
+def _gelu_torch(kind):
+    """The GELU applied at a conv or MLP point: "erf" is torch's exact GELU
+    (npu_whisper_encoder.py:284-287); "poly4" is the reference's poly4 GELU
+    on an fp32 input (g4f: rounded to bf16 RNE, then evaluated with RNE,
+    gelu_row4f.cc:58-84), i.e. what its callers get from ``E.gelu = rt.gelu``
+    (GELU_OP g4r on the fp32 array, rawxrt.py:546-565) and from the device
+    MLP's g4f (rawxrt.py:457); the result is a bf16 value."""
     import torch
     import torch.nn.functional as F
+    from . import bf16 as B
+    if kind == "erf":
+        return F.gelu
+    if kind != "poly4":
+        raise ValueError(f"unknown GELU {kind!r}")
+
+    def poly4(x):
+        bits = R.gelu_poly4(x.numpy(), mode="rne", f32_input=True)
+        return torch.from_numpy(B.to_f32(bits).reshape(x.shape))
+    return poly4
+
+
+def encoder_torch(W, mel, n_layer=None, n_head=None, conv_gelu="erf", mlp_gelu="erf"):
+    """mel fp32 [n_mels, T] or [B, n_mels, T] -> fp32 [ctx, d] or [B, ctx, d].
+    conv_gelu / mlp_gelu: "erf" (default) or "poly4" (see _gelu_torch)."""
+    import torch
+    import torch.nn.functional as F
+    gc, gm = _gelu_torch(conv_gelu), _gelu_torch(mlp_gelu)
 
     nl, nh = geometry(W)
     n_layer = n_layer or nl
@@ -47,9 +70,8 @@ def encoder_torch(W, mel, n_layer=None, n_head=None):
     if squeeze:
         x = x[None]
     with torch.no_grad():
-        x = F.gelu(F.conv1d(x, t["w.conv1.weight"], t["w.conv1.bias"], padding=1))
-        x = F.gelu(F.conv1d(x, t["w.conv2.weight"], t["w.conv2.bias"],
-                            stride=2, padding=1))
+        x = gc(F.conv1d(x, t["w.conv1.weight"], t["w.conv1.bias"], padding=1))
+        x = gc(F.conv1d(x, t["w.conv2.weight"], t["w.conv2.bias"], stride=2, padding=1))
         x = x.permute(0, 2, 1)
         Bn, ctx, d = x.shape
         x = x + t["w.positional_embedding"][:ctx]
@@ -68,7 +90,7 @@ def encoder_torch(W, mel, n_layer=None, n_head=None):
             o = (w @ v).permute(0, 2, 1, 3).reshape(Bn, ctx, d)
             x = x + F.linear(o, t[p + "attn.out.weight"], t[p + "attn.out.bias"])
             h = F.layer_norm(x, (d,), t[p + "mlp_ln.weight"], t[p + "mlp_ln.bias"], 1e-5)
-            f = F.gelu(F.linear(h, t[p + "mlp.0.weight"], t[p + "mlp.0.bias"]))
+            f = gm(F.linear(h, t[p + "mlp.0.weight"], t[p + "mlp.0.bias"]))
             x = x + F.linear(f, t[p + "mlp.2.weight"], t[p + "mlp.2.bias"])
         x = F.layer_norm(x, (d,), t["w.ln_post.weight"], t["w.ln_post.bias"], 1e-5)
     out = x.numpy().astype(np.float32)

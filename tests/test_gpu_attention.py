@@ -14,6 +14,7 @@ import torch
 
 from conftest import case, cosine
 from oracle import bf16 as OB
+from wxhip import _lib as L
 
 pytestmark = pytest.mark.gpu
 
@@ -34,6 +35,14 @@ def _ref(q, k, v, nh, scale):
     return out
 
 
+@pytest.fixture
+def nosplit(dev):
+    """nosplit(True) makes the device's attention launches use the one-part
+    kernel (WXH_TUNE_ATTN_KEYSPLIT); reset after the test."""
+    yield lambda on: dev.set_tuning(L.WXH_TUNE_ATTN_KEYSPLIT, int(on))
+    dev.set_tuning(L.WXH_TUNE_ATTN_KEYSPLIT, 0)
+
+
 def _run(dev, q, k, v, nh, scale, out_dtype=torch.float32):
     B, T, d = q.shape
     f = lambda a: torch.from_numpy(np.ascontiguousarray(a.reshape(B * T, d))).to(dev.device)
@@ -46,10 +55,9 @@ def _run(dev, q, k, v, nh, scale, out_dtype=torch.float32):
 @pytest.mark.parametrize("B,T,nh,mode", [(1, 1500, 20, ""), (2, 512, 6, ""), (1, 100, 2, ""),
                                          (3, 65, 1, ""), (1, 1, 1, ""), (4, 1500, 20, ""),
                                          (1, 1500, 20, "nosplit"), (3, 65, 1, "nosplit")])
-def test_attention_vs_closed_form(dev, B, T, nh, mode, monkeypatch):
+def test_attention_vs_closed_form(dev, B, T, nh, mode, nosplit):
     case(f"attention B={B} T={T} nh={nh} {mode}")
-    if mode == "nosplit":
-        monkeypatch.setenv("WXH_ATTN_NOSPLIT", "1")
+    nosplit(mode == "nosplit")
     rng = np.random.default_rng(T + nh)
     d = nh * 64
     q, k, v = (OB.rb(rng.normal(0, 1, (B, T, d)).astype(np.float32)) for _ in range(3))
@@ -92,15 +100,14 @@ def test_attention_large_logits_masked_tail(dev):
 
 
 @pytest.mark.parametrize("mode", ["", "nosplit"])
-def test_attention_late_max_and_negative_scores(dev, mode, monkeypatch):
+def test_attention_late_max_and_negative_scores(dev, mode, nosplit):
     """The running exp2 reference has to move on a late key block (the last
     50 keys score ~2^30 above the first block's maximum, so that block's
     exps overflow the fast path and are redone), and has to settle far below
     zero when every score is about -80 (identical keys: O = column mean of V).
     Both against the fp64 closed form."""
     case(f"attention late max / negative scores {mode}")
-    if mode == "nosplit":
-        monkeypatch.setenv("WXH_ATTN_NOSPLIT", "1")
+    nosplit(mode == "nosplit")
     B, T, nh = 1, 1500, 2
     d = nh * 64
     rng = np.random.default_rng(8)

@@ -1,11 +1,15 @@
 """The whole encoder on the GPU against the CPU torch fp32 oracle
 (oracle/encoder.py), and the drop-in surface around it.
 
-Gates (cosine over all output elements, synthetic seeded inputs):
+Gates (cosine over all output elements, synthetic seeded inputs), set just
+below what is measured (large-v3: 0.99998; batch items against the same
+mel alone: 0.999992) rather than at the path's floor (0.994 at 32 layers),
+so that a regression shows:
   tiny (4 layers, ctx 1500)          >= 0.9999
   small (12 layers)                  >= 0.9999
-  large-v3 (32 layers, ctx 1500)     >= 0.994
+  large-v3 (32 layers, ctx 1500)     >= 0.9999
   reduced context (ctx 512)          >= 0.9999
+  batched vs the same mel alone      >= 0.99999
 Size-independent properties: batch item b of a batched forward equals the
 same mel run alone, bit for bit (for batch sizes that pick the same GEMM
 split, as batch 1 and 3 of tiny do); graph replay equals eager launch, bit
@@ -111,7 +115,7 @@ def test_large_v3_encoder_cosine(dev, large):
     c = cosine(got, ref)
     report("large_v3_encoder", cosine=c, max_abs=float(np.abs(got - ref).max()))
     assert got.shape == (1500, 1280) and np.isfinite(got).all()
-    assert c >= 0.994
+    assert c >= 0.9999
 
 
 def test_large_v3_batch16_bench_workload(dev, large):
@@ -134,8 +138,8 @@ def test_large_v3_batch16_bench_workload(dev, large):
     c_ref = [cosine(got[b], OE.encoder_torch(large, mels[b])) for b in (0, 15)]
     report("large_v3_batch16", cosine_batched_vs_single_min=min(c_items),
            cosine_vs_oracle=c_ref)
-    assert min(c_ref) >= 0.994, c_ref
-    assert min(c_items) >= 0.999, c_items
+    assert min(c_ref) >= 0.9999, c_ref
+    assert min(c_items) >= 0.99999, c_items
 
 
 def test_large_v3_batch16_ctx512(dev, large):
@@ -153,11 +157,11 @@ def test_large_v3_batch16_ctx512(dev, large):
     c_ref = [cosine(got[b], OE.encoder_torch(large, mels[b])) for b in (0, 15)]
     report("large_v3_batch16_ctx512", cosine_batched_vs_single_min=min(c_items),
            cosine_vs_oracle=c_ref)
-    assert min(c_ref) >= 0.994, c_ref
-    assert min(c_items) >= 0.999, c_items
+    assert min(c_ref) >= 0.9999, c_ref
+    assert min(c_items) >= 0.99999, c_items
 
 
-def test_split_k_batch1(dev, large, monkeypatch):
+def test_split_k_batch1(dev, large):
     """At batch 1 the large-v3 fc2 (K 5120) and conv2 (K 3840) GEMMs have
     120 output tiles of 128x128 and split K over two workgroups per tile.
     The result does not depend on which workgroup of a tile finishes last
@@ -168,14 +172,16 @@ def test_split_k_batch1(dev, large, monkeypatch):
     a = _fwd(_enc(dev, large, n_layer=2), mel, dev)
     b = _fwd(_enc(dev, large, n_layer=2), mel, dev)
     np.testing.assert_array_equal(a, b)
-    monkeypatch.setenv("WXH_GEMM_SPLITK", "1")
-    c = _fwd(_enc(dev, large, n_layer=2), mel, dev)
-    monkeypatch.delenv("WXH_GEMM_SPLITK")
+    dev.set_tuning(L.WXH_TUNE_GEMM_SPLITK, 1)     # encoders made now never split
+    try:
+        c = _fwd(_enc(dev, large, n_layer=2), mel, dev)
+    finally:
+        dev.set_tuning(L.WXH_TUNE_GEMM_SPLITK, 0)
     ref = OE.encoder_torch(large, mel, n_layer=2)
     c_split, c_plain = cosine(a, ref), cosine(c, ref)
     report("split_k_batch1", cosine_split_vs_plain=cosine(a, c), cosine_split=c_split,
            cosine_plain=c_plain, max_abs_split_vs_plain=float(np.abs(a - c).max()))
-    assert not np.array_equal(a, c), "WXH_GEMM_SPLITK=1 should change the summation order"
+    assert not np.array_equal(a, c), "not splitting should change the summation order"
     assert cosine(a, c) >= 0.99999
     assert c_split >= 0.9999 and c_plain >= 0.9999
 
@@ -280,3 +286,69 @@ def test_encoder_from_ref_npz(dev, tiny, tmp_path):
     a = _fwd(_enc(dev, tiny), mel, dev)
     b = _fwd(wxhip.HipEncoder.from_file(dev, p), mel2, dev)
     np.testing.assert_array_equal(a, b)
+
+
+def test_calls_on_two_streams_are_ordered(dev, tiny):
+    """An encoder's calls share its workspace. A batch-16 forward on torch's
+    stream followed at once (no host sync) by a batch-1 forward_numpy on the
+    library's stream, and a batch-1 forward followed at once by a batch-4 one
+    that has to grow the workspace, give what the same calls give with a sync
+    between them."""
+    case("encoder calls on two streams / workspace regrow, unsynced")
+    mels = synth.make_mel_batch(16, 80, 3000)
+    enc = _enc(dev, tiny)
+    m16 = torch.from_numpy(mels).to(dev.device)
+    want16 = _fwd(enc, mels, dev)
+    want1 = enc.forward_numpy(mels[3])
+    got16 = enc.forward(m16)                 # torch's stream, not waited for
+    got1 = enc.forward_numpy(mels[3])        # library stream, host buffers
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got1, want1)
+    np.testing.assert_array_equal(got16.cpu().numpy(), want16)
+    # batch 1 and batch 4 pick other GEMM tiles than batch 16 (another fp32
+    # summation order), so they are compared with synced runs of their own
+    want_a = _fwd(_enc(dev, tiny), mels[5:6], dev)
+    want_b = _fwd(_enc(dev, tiny), mels[:4], dev)
+    enc2 = _enc(dev, tiny)
+    a = enc2.forward(m16[5:6])               # workspace sized for batch 1
+    b = enc2.forward(m16[:4])                # regrow while batch 1 may still run
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(a.cpu().numpy(), want_a)
+    np.testing.assert_array_equal(b.cpu().numpy(), want_b)
+
+
+def test_forward_host_deadline(dev, large):
+    """wxh_set_timeout bounds forward_host's wait (NPU_RUN_TIMEOUT_MS): a
+    1 ms deadline on a 32-layer large-v3 forward (about 5 ms of device work)
+    returns WXH_ERR_TIMEOUT with the caller's output untouched, while the
+    kernels run to completion; the next call, with no deadline, is exact."""
+    import wxhip
+    case("forward_host deadline (large-v3 32 layers, batch 1)")
+    own = wxhip.Device(0)
+    enc = wxhip.HipEncoder(own, large)
+    mel = synth.make_mel(128, 3000, seed=11)
+    want = enc.forward_numpy(mel)            # graph built, no deadline
+    out = np.full((1, 1500, 1280), np.nan, np.float32)
+    own.set_timeout(1)
+    import ctypes as C
+    rc = own.lib.wxh_encoder_forward_host(enc._h, np.ascontiguousarray(mel[None]).ctypes.data_as(
+        C.c_void_p), 1, 3000, out.ctypes.data_as(C.c_void_p))
+    assert rc == L.WXH_ERR_TIMEOUT, (rc, own.lib.wxh_last_error())
+    assert b"1 ms" in own.lib.wxh_last_error()
+    assert np.isnan(out).all()               # nothing written into the caller's buffer
+    own.set_timeout(0)
+    own.wait()
+    np.testing.assert_array_equal(enc.forward_numpy(mel), want)
+    # the deadline applies to wxh_synchronize too: a long queue, 1 ms
+    m = torch.from_numpy(mel[None]).to(own.device)
+    for _ in range(4):
+        enc.forward(m)
+    own.set_timeout(1)
+    with pytest.raises(L.WxhError) as ei:
+        enc.forward_numpy(mel)
+    assert ei.value.code == L.WXH_ERR_TIMEOUT
+    own.set_timeout(0)
+    own.wait()
+    torch.cuda.synchronize()
+    enc.close()
+    own.close()

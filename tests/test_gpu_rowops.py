@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import bits, case, to_dev_bf16
+from conftest import bits, case, report, to_dev_bf16
 from oracle import bf16 as OB
 from oracle import rowops as OR
 from wxhip import _lib as L
@@ -41,7 +41,11 @@ def _ln_check(got_bits, x, g=None, b=None):
     err = np.abs(OB.to_f32(got_bits).astype(np.float64) - exact)
     ok2 = (np.abs(exact) < 2 ** -7 * mag) & (err <= 2 ** -16 * mag)
     assert (ok1 | ok2).all(), f"max {d[~(ok1 | ok2)].max()} ulp outside the bound"
-    return int((~ok1).sum())
+    n = int((~ok1).sum())
+    # the allowance is for isolated cancellations, not a looser gate: at most
+    # 0.1 % of the elements may need it
+    assert n <= 1e-3 * d.size, f"{n} of {d.size} elements needed the cancellation allowance"
+    return n
 
 
 @pytest.fixture(scope="module")
@@ -55,7 +59,8 @@ def test_layernorm_bf16_affine_rowop_shape(dev, inputs):
     g, b = inputs["ln_gamma"], inputs["ln_beta"]
     y = dev.layer_norm(to_dev_bf16(x, dev), torch.from_numpy(g).to(dev.device),
                        torch.from_numpy(b).to(dev.device))
-    _ln_check(bits(y), x, g, b)
+    n = _ln_check(bits(y), x, g, b)
+    report("layernorm_rowop_shape_allowance", elements=int(x.size), allowance=n)
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 8), (7, 384), (33, 768), (1500, 1280), (5, 4096)])

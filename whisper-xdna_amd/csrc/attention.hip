@@ -359,15 +359,14 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
 hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
                             const uint16_t* Vt, int batch, int n_head, int T,
                             float scale, void* O, int o_dtype, int64_t ldo,
-                            hipStream_t s, bool q_prescaled) {
+                            hipStream_t s, bool q_prescaled, int keysplit) {
   if (T <= 0 || batch <= 0 || n_head <= 0) return hipSuccess;
   const int Tp = attn_padded_len(T);
   dim3 grid((T + kQB - 1) / kQB, n_head, batch);
   const float scale_log2 = attn_q_scale(scale);
   // Fewer workgroups than CUs (batch 1: 20 heads x 12 query blocks): split
   // every workgroup's keys over twice the waves, halving each wave's walk.
-  const bool split =
-      (int64_t)grid.x * grid.y * grid.z < 256 && getenv("WXH_ATTN_NOSPLIT") == nullptr;
+  const bool split = (int64_t)grid.x * grid.y * grid.z < 256 && keysplit != 1;
   const bool f32 = o_dtype == DT_F32;
 #define WX_ATTN(F32, KS, QP)                                                            \
   if (f32 == F32 && (KS == 2) == split && q_prescaled == QP)                           \

@@ -16,9 +16,11 @@
 #include <cstdlib>
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cstring>
 #include <map>
 #include <string>
+#include <thread>
 #include <utility>
 #include <vector>
 
@@ -69,6 +71,9 @@ struct wxh_ctx {
   int* logmel_slots = nullptr;     // per-clip maxima scratch of wxh_log_mel
   int logmel_cap = 0;              // clips it holds
   unsigned* absmax_bits = nullptr; // per-tensor scale scratch of wxh_quantize_rows
+  int timeout_ms = 0;              // deadline of the library's blocking waits (0: none)
+  int tune_splitk = 0;             // WXH_TUNE_GEMM_SPLITK
+  int tune_attn_keysplit = 0;      // WXH_TUNE_ATTN_KEYSPLIT
 };
 
 namespace {
@@ -76,6 +81,40 @@ namespace {
 // NULL is HIP's default (null) stream, exactly as in the HIP API; the
 // context's own stream is available through wxh_get_stream().
 hipStream_t pick(wxh_ctx*, void* s) { return static_cast<hipStream_t>(s); }
+
+// Wait on the host until `ev` has completed, polling it, for at most
+// timeout_ms (0: no deadline). The device work is never cancelled.
+int wait_event(hipEvent_t ev, int timeout_ms, const char* what) {
+  if (timeout_ms <= 0) {
+    hipError_t e = hipEventSynchronize(ev);
+    if (e != hipSuccess) return fail(WXH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return WXH_OK;
+  }
+  using clk = std::chrono::steady_clock;
+  const auto deadline = clk::now() + std::chrono::milliseconds(timeout_ms);
+  for (;;) {
+    const hipError_t e = hipEventQuery(ev);
+    if (e == hipSuccess) return WXH_OK;
+    if (e != hipErrorNotReady)
+      return fail(WXH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    if (clk::now() >= deadline)
+      return fail(WXH_ERR_TIMEOUT, "%s: not complete after %d ms (the device work continues)",
+                  what, timeout_ms);
+    std::this_thread::sleep_for(std::chrono::microseconds(50));
+  }
+}
+
+// Record an event on `s` and wait for it under the deadline.
+int wait_stream(hipStream_t s, int timeout_ms, const char* what) {
+  hipEvent_t ev;
+  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e != hipSuccess) return fail(WXH_ERR_HIP, "%s: hipEventCreate: %s", what, hipGetErrorString(e));
+  e = hipEventRecord(ev, s);
+  int r = e == hipSuccess ? wait_event(ev, timeout_ms, what)
+                          : fail(WXH_ERR_HIP, "%s: hipEventRecord: %s", what, hipGetErrorString(e));
+  (void)hipEventDestroy(ev);
+  return r;
+}
 
 int check_ctx(wxh_ctx* c, uint32_t bit, const char* what) {
   if (!c) return fail(WXH_ERR_INVALID, "%s: null context", what);
@@ -159,8 +198,30 @@ int wxh_get_stream(wxh_ctx* c, void** stream) {
 int wxh_synchronize(wxh_ctx* c) {
   WXH_REQUIRE(c, "wxh_synchronize: null context");
   WXH_HIP(hipSetDevice(c->device));
-  WXH_HIP(hipStreamSynchronize(c->stream));
+  return wait_stream(c->stream, c->timeout_ms, "wxh_synchronize");
+}
+
+int wxh_set_timeout(wxh_ctx* c, int timeout_ms) {
+  WXH_REQUIRE(c && timeout_ms >= 0, "wxh_set_timeout: null context or negative deadline");
+  c->timeout_ms = timeout_ms;
   return WXH_OK;
+}
+
+int wxh_set_tuning(wxh_ctx* c, int what, int value) {
+  WXH_REQUIRE(c, "wxh_set_tuning: null context");
+  WXH_REQUIRE(value >= 0, "wxh_set_tuning: negative value %d", value);
+  switch (what) {
+    case WXH_TUNE_GEMM_SPLITK:
+      WXH_REQUIRE(value <= 8, "wxh_set_tuning: split count %d > 8", value);
+      c->tune_splitk = value;
+      return WXH_OK;
+    case WXH_TUNE_ATTN_KEYSPLIT:
+      WXH_REQUIRE(value <= 1, "wxh_set_tuning: key split mode %d (0 or 1)", value);
+      c->tune_attn_keysplit = value;
+      return WXH_OK;
+    default:
+      return fail(WXH_ERR_INVALID, "wxh_set_tuning: unknown switch %d", what);
+  }
 }
 
 // ------------------------------------------------------------------ row ops
@@ -391,7 +452,7 @@ int wxh_attention(wxh_ctx* c, const uint16_t* Q, const uint16_t* K,
   WXH_REQUIRE(aligned16(Q) && aligned16(K) && aligned16(Vt) && aligned16(O),
               "wxh_attention: operands must be 16-byte aligned");
   WXH_HIP(wx::launch_attention(Q, K, Vt, batch, n_head, T, scale, O, o_dtype, ldo,
-                               pick(c, stream)));
+                               pick(c, stream), false, c->tune_attn_keysplit));
   return WXH_OK;
 }
 
@@ -471,6 +532,22 @@ struct wxh_encoder {
   std::vector<void*> ws_allocs;
   bool use_graph = true;
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+  // Calls share the workspace. `done` is recorded on a forward's stream at
+  // its end: a forward on another stream first makes its stream wait for
+  // it, and whatever frees or rewrites memory a forward reads (workspace
+  // regrow, weights, graphs, the staging buffers, destroy) waits for it on
+  // the host.
+  hipEvent_t done = nullptr;
+  bool done_pending = false;
+  hipStream_t last_stream = nullptr;
+  int tune_splitk = 0, tune_attn_keysplit = 0;  // the context's, at creation
+  // wxh_encoder_forward_host staging: pinned host and device copies of the
+  // mel and the features, grown to the largest call
+  float* h_mel = nullptr;
+  float* h_out = nullptr;
+  float* d_mel = nullptr;
+  float* d_out = nullptr;
+  size_t cap_io_in = 0, cap_io_out = 0;
   // int8 GEMM path
   bool i8_weights = false;   // int8 weight copies are kept (enable_int8)
   bool i8 = false;           // the forward runs the int8 path (set_int8)
@@ -509,6 +586,15 @@ int dalloc(std::vector<void*>& list, T** p, size_t count, bool zero) {
 void free_list(std::vector<void*>& list) {
   for (void* p : list) (void)hipFree(p);
   list.clear();
+}
+
+// Host wait for the encoder's last forward; bounded by the context's
+// deadline unless `bounded` is false (before memory is freed).
+int quiesce(wxh_encoder* E, const char* what, bool bounded = true) {
+  if (!E->done_pending) return WXH_OK;
+  const int r = wait_event(E->done, bounded ? E->ctx->timeout_ms : 0, what);
+  if (r == WXH_OK) E->done_pending = false;
+  return r;
 }
 
 void drop_graphs(wxh_encoder* E) {
@@ -597,6 +683,7 @@ int ensure_workspace(wxh_encoder* E, int batch, int frames) {
       need_qkv <= E->cap_qkv && need_f <= E->cap_f && need_aq <= E->cap_aq &&
       need_asc <= E->cap_asc && need_f32 <= E->cap_f32)
     return WXH_OK;
+  if (int r = quiesce(E, "encoder workspace regrow", false)) return r;
   drop_graphs(E);
   free_list(E->ws_allocs);
   E->cap_mel = E->cap_x1 = E->cap_x = E->cap_qkv = E->cap_f = 0;
@@ -638,6 +725,7 @@ void set_splitk(wxh_encoder* E, wx::EpiParams& e) {
   e.sk_ws_elems = kSplitKElems;
   e.sk_cnt = E->sk_cnt;
   e.sk_cnt_len = kSplitKTiles;
+  e.force_splits = E->tune_splitk;
 }
 
 // Zero rows 0 and T+1 of every batch item of the padded conv1 output (the
@@ -728,7 +816,7 @@ int run_body_i8(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer
       if (int r = mark(ST_QKV)) return r;
     }
     WXH_HIP(wx::launch_attention(E->q, E->k, E->vt, batch, nh, ctx, scale, E->f32ws,
-                                 wx::DT_F32, d, s, true));
+                                 wx::DT_F32, d, s, true, E->tune_attn_keysplit));
     if (int r = mark(ST_ATTN)) return r;
     {
       WXH_HIP(wx::launch_quantize_rows(E->f32ws, wx::DT_F32, d, M, d, E->aq, d, d, E->asc,
@@ -773,6 +861,7 @@ int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* t
   const int ctx = (T - 1) / 2 + 1;
   const int tp = wx::attn_padded_len(ctx);
   const int M = batch * ctx;
+  const int conv_gelu = D.conv_gelu == WXH_GELU_POLY4_RNE ? wx::GELU_POLY4_RNE : wx::GELU_ERF;
   auto mark = [&](int stage) -> int {
     if (!timer) return WXH_OK;
     hipEvent_t ev;
@@ -788,6 +877,7 @@ int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* t
     e.out = E->x1;
     e.ldo = d;
     e.bias = E->conv1_b;
+    e.gelu = conv_gelu;
     e.rows_per_batch = T;
     e.out_batch_stride = (int64_t)(T + 2) * d;
     WXH_HIP(wx::launch_gemm(batch * T, d, 3 * D.n_mels, a, E->conv1_w, 3 * D.n_mels,
@@ -800,6 +890,7 @@ int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* t
     e.out = E->x;
     e.ldo = d;
     e.bias = E->conv2_b;
+    e.gelu = conv_gelu;
     e.aux = E->pos;
     e.rows_per_batch = ctx;
     set_splitk(E, e);
@@ -828,7 +919,7 @@ int run_body(wxh_encoder* E, int batch, int frames, hipStream_t s, StageTimer* t
       if (int r = mark(ST_QKV)) return r;
     }
     WXH_HIP(wx::launch_attention(E->q, E->k, E->vt, batch, nh, ctx, scale, E->o,
-                                 wx::DT_BF16, d, s, true));
+                                 wx::DT_BF16, d, s, true, E->tune_attn_keysplit));
     if (int r = mark(ST_ATTN)) return r;
     {
       wx::GemmA a{E->o, d, M, 0};
@@ -884,6 +975,7 @@ int forward_impl(wxh_encoder* E, const float* mel, int batch, int frames, float*
   const auto& D = E->dims;
   const int ctx = (frames - 1) / 2 + 1;
   if (int r = ensure_workspace(E, batch, frames)) return r;
+  if (E->done_pending && s != E->last_stream) WXH_HIP(hipStreamWaitEvent(s, E->done, 0));
   if (E->i8) {
     WXH_HIP(wx::launch_transpose_f32(mel, batch, D.n_mels, frames, E->f32ws, s));
   } else {
@@ -934,6 +1026,35 @@ int forward_impl(wxh_encoder* E, const float* mel, int batch, int frames, float*
     WXH_HIP(hipEventRecord(ev, s));
     timer->marks.push_back({ST_LNPOST, ev});
   }
+  WXH_HIP(hipEventRecord(E->done, s));
+  E->done_pending = true;
+  E->last_stream = s;
+  return WXH_OK;
+}
+
+// Pinned host and device staging of wxh_encoder_forward_host, grown (after
+// the last forward has finished with them) to n_in / n_out floats.
+int ensure_io_staging(wxh_encoder* E, size_t n_in, size_t n_out) {
+  if (n_in <= E->cap_io_in && n_out <= E->cap_io_out) return WXH_OK;
+  if (int r = quiesce(E, "wxh_encoder_forward_host staging regrow")) return r;
+  if (n_in > E->cap_io_in) {
+    if (E->h_mel) (void)hipHostFree(E->h_mel);
+    if (E->d_mel) (void)hipFree(E->d_mel);
+    E->h_mel = E->d_mel = nullptr;
+    E->cap_io_in = 0;
+    WXH_HIP(hipHostMalloc((void**)&E->h_mel, n_in * sizeof(float), hipHostMallocDefault));
+    WXH_HIP(hipMalloc(&E->d_mel, n_in * sizeof(float)));
+    E->cap_io_in = n_in;
+  }
+  if (n_out > E->cap_io_out) {
+    if (E->h_out) (void)hipHostFree(E->h_out);
+    if (E->d_out) (void)hipFree(E->d_out);
+    E->h_out = E->d_out = nullptr;
+    E->cap_io_out = 0;
+    WXH_HIP(hipHostMalloc((void**)&E->h_out, n_out * sizeof(float), hipHostMallocDefault));
+    WXH_HIP(hipMalloc(&E->d_out, n_out * sizeof(float)));
+    E->cap_io_out = n_out;
+  }
   return WXH_OK;
 }
 
@@ -953,9 +1074,16 @@ int wxh_encoder_create(wxh_ctx* c, const wxh_encoder_dims* dims, wxh_encoder** o
   WXH_REQUIRE(D.d_model <= wx::kMaxRowCols, "wxh_encoder_create: d_model too large");
   WXH_REQUIRE(D.mlp_gelu == WXH_GELU_ERF || D.mlp_gelu == WXH_GELU_POLY4_RNE,
               "wxh_encoder_create: mlp_gelu must be ERF or POLY4_RNE");
+  WXH_REQUIRE(D.conv_gelu == WXH_GELU_ERF || D.conv_gelu == WXH_GELU_POLY4_RNE,
+              "wxh_encoder_create: conv_gelu must be ERF or POLY4_RNE");
+  hipEvent_t done = nullptr;
+  WXH_HIP(hipEventCreateWithFlags(&done, hipEventDisableTiming));
   auto* E = new wxh_encoder;
   E->ctx = c;
   E->dims = D;
+  E->done = done;
+  E->tune_splitk = c->tune_splitk;
+  E->tune_attn_keysplit = c->tune_attn_keysplit;
   E->ffn = 4 * D.d_model;
   const int d = D.d_model, ffn = E->ffn;
   auto& A = E->allocs;
@@ -984,6 +1112,7 @@ int wxh_encoder_create(wxh_ctx* c, const wxh_encoder_dims* dims, wxh_encoder** o
   }
   if (r != WXH_OK) {
     free_list(E->allocs);
+    (void)hipEventDestroy(E->done);
     delete E;
     return r;
   }
@@ -995,11 +1124,17 @@ int wxh_encoder_create(wxh_ctx* c, const wxh_encoder_dims* dims, wxh_encoder** o
 int wxh_encoder_destroy(wxh_encoder* E) {
   if (!E) return WXH_OK;
   (void)hipSetDevice(E->ctx->device);
+  (void)quiesce(E, "wxh_encoder_destroy", false);
   (void)hipStreamSynchronize(E->ctx->stream);
   drop_graphs(E);
   free_list(E->ws_allocs);
   free_list(E->allocs);
   if (E->stage) (void)hipFree(E->stage);
+  if (E->h_mel) (void)hipHostFree(E->h_mel);
+  if (E->h_out) (void)hipHostFree(E->h_out);
+  if (E->d_mel) (void)hipFree(E->d_mel);
+  if (E->d_out) (void)hipFree(E->d_out);
+  (void)hipEventDestroy(E->done);
   wxh_ctx* c = E->ctx;
   delete E;
   ctx_release(c);
@@ -1010,6 +1145,7 @@ int wxh_encoder_set_weight(wxh_encoder* E, const char* name, const float* host,
                            const int64_t* shape, int ndim) {
   WXH_REQUIRE(E && name && host && shape, "wxh_encoder_set_weight: null argument");
   if (int r = check_ctx(E->ctx, 0, "wxh_encoder_set_weight")) return r;
+  if (int r = quiesce(E, "wxh_encoder_set_weight", false)) return r;  // a forward may read it
   std::string n = name;
   if (n.rfind("w.", 0) == 0) n = n.substr(2);
   const auto& D = E->dims;
@@ -1116,8 +1252,8 @@ int wxh_encoder_enable_int8(wxh_encoder* E) {
   if (D.d_model % wx::kI8KAlign != 0)
     return fail(WXH_ERR_UNSUPPORTED, "wxh_encoder_enable_int8: d_model=%d is not a multiple "
                 "of %d", D.d_model, wx::kI8KAlign);
-  if (D.mlp_gelu != WXH_GELU_ERF)
-    return fail(WXH_ERR_UNSUPPORTED, "wxh_encoder_enable_int8: needs the erf MLP GELU");
+  if (D.mlp_gelu != WXH_GELU_ERF || D.conv_gelu != WXH_GELU_ERF)
+    return fail(WXH_ERR_UNSUPPORTED, "wxh_encoder_enable_int8: needs the erf MLP and conv GELUs");
   const int d = D.d_model, ffn = E->ffn;
   E->k1p = (3 * D.n_mels + wx::kI8KAlign - 1) / wx::kI8KAlign * wx::kI8KAlign;
   auto& A = E->allocs;
@@ -1147,7 +1283,7 @@ int wxh_encoder_set_int8(wxh_encoder* E, int on) {
     return fail(WXH_ERR_STATE, "wxh_encoder_set_int8: wxh_encoder_enable_int8 was not called "
                 "before the weights were set");
   if ((on != 0) != E->i8) {
-    (void)hipStreamSynchronize(E->ctx->stream);
+    if (int r = quiesce(E, "wxh_encoder_set_int8", false)) return r;
     drop_graphs(E);
     E->i8 = on != 0;
   }
@@ -1169,28 +1305,22 @@ int wxh_encoder_forward_host(wxh_encoder* E, const float* mel_host, int batch,
   const int ctx = (frames - 1) / 2 + 1;
   const size_t n_in = (size_t)batch * D.n_mels * frames;
   const size_t n_out = (size_t)batch * ctx * D.d_model;
-  float *dm = nullptr, *dout = nullptr;
-  WXH_HIP(hipMalloc(&dm, n_in * sizeof(float)));
-  hipError_t e = hipMalloc(&dout, n_out * sizeof(float));
-  if (e != hipSuccess) {
-    (void)hipFree(dm);
-    return fail(WXH_ERR_HIP, "hipMalloc: %s", hipGetErrorString(e));
-  }
+  if (int r = ensure_io_staging(E, n_in, n_out)) return r;
+  // a forward that timed out earlier may still be reading the staging
+  if (int r = quiesce(E, "wxh_encoder_forward_host")) return r;
   hipStream_t s = E->ctx->stream;
-  int r = WXH_OK;
-  e = hipMemcpyAsync(dm, mel_host, n_in * sizeof(float), hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) r = fail(WXH_ERR_HIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
-  if (r == WXH_OK) r = forward_impl(E, dm, batch, frames, dout, s, nullptr);
-  if (r == WXH_OK) {
-    e = hipMemcpyAsync(out_host, dout, n_out * sizeof(float), hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) r = fail(WXH_ERR_HIP, "copy out: %s", hipGetErrorString(e));
-  } else {
-    (void)hipStreamSynchronize(s);
+  std::memcpy(E->h_mel, mel_host, n_in * sizeof(float));
+  WXH_HIP(hipMemcpyAsync(E->d_mel, E->h_mel, n_in * sizeof(float), hipMemcpyHostToDevice, s));
+  if (int r = forward_impl(E, E->d_mel, batch, frames, E->d_out, s, nullptr)) {
+    (void)wait_stream(s, E->ctx->timeout_ms, "wxh_encoder_forward_host");
+    return r;
   }
-  (void)hipFree(dm);
-  (void)hipFree(dout);
-  return r;
+  WXH_HIP(hipMemcpyAsync(E->h_out, E->d_out, n_out * sizeof(float), hipMemcpyDeviceToHost, s));
+  WXH_HIP(hipEventRecord(E->done, s));  // the copy out is part of this call
+  E->done_pending = true;
+  if (int r = quiesce(E, "wxh_encoder_forward_host")) return r;
+  std::memcpy(out_host, E->h_out, n_out * sizeof(float));
+  return WXH_OK;
 }
 
 int wxh_encoder_profile(wxh_encoder* E, const float* mel, int batch, int frames,
@@ -1202,7 +1332,8 @@ int wxh_encoder_profile(wxh_encoder* E, const float* mel, int batch, int frames,
   WXH_HIP(hipEventCreate(&t.start));
   WXH_HIP(hipEventRecord(t.start, s));
   int r = forward_impl(E, mel, batch, frames, out, s, &t);
-  hipError_t e = hipStreamSynchronize(s);
+  const int w = wait_stream(s, E->ctx->timeout_ms, "wxh_encoder_profile");
+  const hipError_t e = w == WXH_OK ? hipSuccess : hipErrorNotReady;
   std::vector<float> acc(ST_COUNT, 0.f);
   hipEvent_t prev = t.start;
   for (auto& m : t.marks) {
@@ -1214,7 +1345,7 @@ int wxh_encoder_profile(wxh_encoder* E, const float* mel, int batch, int frames,
   for (auto& m : t.marks) (void)hipEventDestroy(m.second);
   (void)hipEventDestroy(t.start);
   if (r != WXH_OK) return r;
-  if (e != hipSuccess) return fail(WXH_ERR_HIP, "profile sync: %s", hipGetErrorString(e));
+  if (w != WXH_OK) return w;
   for (int i = 0; i < n; ++i) ms[i] = i < ST_COUNT ? acc[i] : 0.f;
   return WXH_OK;
 }

@@ -18,9 +18,6 @@
 //   C: lane l holds column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4
 // The epilogue is fused: bias, GELU, residual add, the conv front end's
 // padded output and positional embedding, and the QKV head split.
-#include <cstdio>
-#include <cstdlib>
-#include <string>
 #include <utility>
 
 #include "common.h"
@@ -32,6 +29,16 @@ namespace wx {
 // the fp32 accumulator rounded to bf16 (RNE), then the RNE evaluation).
 __device__ __forceinline__ float epi_poly4(float xin) {
   return poly4_gelu_pre<true>(rb_rne(xin));
+}
+
+// The GELU of a conv epilogue mode: poly4 (g4f) for the *_POLY4 modes,
+// else erf.
+template <int MODE>
+__device__ __forceinline__ float conv_act(float x) {
+  if constexpr (MODE == EPI_CONV1_POLY4 || MODE == EPI_CONV2_POLY4)
+    return epi_poly4(x);
+  else
+    return gelu_erf(x);
 }
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
@@ -131,10 +138,11 @@ __device__ __forceinline__ void store_tile(const EpiParams& e, const f32x16 (&ac
             float* p = static_cast<float*>(e.out) + r0[r] + cofs[j];
             *p = *p + x;
           } else if (MODE == EPI_CONV1) {
-            static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(gelu_erf(x));
+            x = e.gelu == GELU_POLY4_RNE ? epi_poly4(x) : gelu_erf(x);
+            static_cast<uint16_t*>(e.out)[r0[r] + cofs[j]] = f2bf(x);
           } else if (MODE == EPI_CONV2) {
-            static_cast<float*>(e.out)[r0[r] + cofs[j]] =
-                gelu_erf(x) + e.aux[(int64_t)tt[r] * N + cofs[j]];
+            x = e.gelu == GELU_POLY4_RNE ? epi_poly4(x) : gelu_erf(x);
+            static_cast<float*>(e.out)[r0[r] + cofs[j]] = x + e.aux[(int64_t)tt[r] * N + cofs[j]];
           } else {  // EPI_QKV
             const uint16_t val = f2bf(which[j] == 0 ? x * e.q_scale : x);
             if (which[j] == 0)
@@ -202,11 +210,11 @@ __device__ __forceinline__ void store_tile_t_impl(const EpiParams& e, const f32x
     if (CHECKED && m >= M) return;
     int t = m;
     int64_t r0, r1 = 0;
-    if (MODE == EPI_CONV1 || MODE == EPI_CONV2 || MODE == EPI_QKV) {
+    if (epi_conv1(MODE) || epi_conv2(MODE) || MODE == EPI_QKV) {
       const int T = e.rows_per_batch;
       const int b = m / T;
       t = m - b * T;
-      if (MODE == EPI_CONV1) {
+      if (epi_conv1(MODE)) {
         r0 = (int64_t)b * e.out_batch_stride + (int64_t)(t + 1) * e.ldo;
       } else if (MODE == EPI_QKV) {
         r0 = ((int64_t)b * e.n_head * e.t_pad + t) * 64;
@@ -217,12 +225,12 @@ __device__ __forceinline__ void store_tile_t_impl(const EpiParams& e, const f32x
     } else {
       r0 = (int64_t)m * e.ldo;
     }
-    // The residual (EPI_RESID) or positional embedding (EPI_CONV2) of this
+    // The residual (EPI_RESID) or positional embedding (EPI_CONV2*) of this
     // block row is read in one batch before any of its stores: issued after
     // a store, each load would wait out a full memory round trip on its own
     // (the compiler cannot move loads above stores that may alias).
     f32x4 pre[TN][4];
-    if (!CHECKED && (MODE == EPI_RESID || MODE == EPI_CONV2)) {
+    if (!CHECKED && (MODE == EPI_RESID || epi_conv2(MODE))) {
       static_for<TN>([&](auto j) {
         static_for<4>([&](auto g) {
           const int n0 = col0 + j * 32 + g * 8 + half * 4;
@@ -240,22 +248,23 @@ __device__ __forceinline__ void store_tile_t_impl(const EpiParams& e, const f32x
         float x[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = acc[i][j][g * 4 + r] + bv[j][g][r];
-        if (MODE == EPI_F32 || MODE == EPI_RESID || MODE == EPI_CONV2) {
+        if (MODE == EPI_F32 || MODE == EPI_RESID || epi_conv2(MODE)) {
           float* p = static_cast<float*>(e.out) + r0 + n0;
           if (!CHECKED) {
             f32x4 v = {x[0], x[1], x[2], x[3]};
-            if (MODE == EPI_CONV2) {
+            if (epi_conv2(MODE)) {
 #pragma unroll
-              for (int r = 0; r < 4; ++r) v[r] = gelu_erf(v[r]) + pre[j][g][r];
+              for (int r = 0; r < 4; ++r) v[r] = conv_act<MODE>(v[r]) + pre[j][g][r];
             }
             if (MODE == EPI_RESID) v += pre[j][g];
             *reinterpret_cast<f32x4*>(p) = v;
             return;
           }
-          if (MODE == EPI_CONV2) {
+          if (epi_conv2(MODE)) {
             const float* ap = e.aux + (int64_t)t * N + n0;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x[r] = gelu_erf(x[r]) + (full || n0 + r < N ? ap[r] : 0.f);
+            for (int r = 0; r < 4; ++r)
+              x[r] = conv_act<MODE>(x[r]) + (full || n0 + r < N ? ap[r] : 0.f);
           }
           if (full && v32) {
             f32x4 v = {x[0], x[1], x[2], x[3]};
@@ -267,10 +276,11 @@ __device__ __forceinline__ void store_tile_t_impl(const EpiParams& e, const f32x
               if (n0 + r < N) p[r] = MODE == EPI_RESID ? p[r] + x[r] : x[r];
           }
         } else if (MODE == EPI_BF16 || MODE == EPI_BF16_GELU || MODE == EPI_BF16_POLY4 ||
-                   MODE == EPI_CONV1) {
+                   epi_conv1(MODE)) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (MODE == EPI_CONV1 || MODE == EPI_BF16_GELU) x[r] = gelu_erf(x[r]);
+            if (epi_conv1(MODE)) x[r] = conv_act<MODE>(x[r]);
+            if (MODE == EPI_BF16_GELU) x[r] = gelu_erf(x[r]);
             if (MODE == EPI_BF16_POLY4) x[r] = epi_poly4(x[r]);
           }
           uint16_t* p = static_cast<uint16_t*>(e.out) + r0 + n0;
@@ -309,8 +319,8 @@ __device__ __forceinline__ void store_tile_t(const EpiParams& e, const f32x16 (&
   const uintptr_t ob = (uintptr_t)e.out;
   const bool aligned = (e.ldo & 3) == 0 && (ob & 15) == 0;
   const bool interior = row0 + TM * 32 <= M && col0 + TN * 32 <= N &&
-                        (MODE == EPI_QKV || MODE == EPI_CONV1 || aligned) &&
-                        (MODE != EPI_CONV2 || (N & 3) == 0);
+                        (MODE == EPI_QKV || epi_conv1(MODE) || aligned) &&
+                        (!epi_conv2(MODE) || (N & 3) == 0);
   if (interior)
     store_tile_t_impl<MODE, TM, TN, false>(e, acc, bv, M, N, row0, col0, lane);
   else
@@ -752,8 +762,7 @@ template <class C, int MODE, bool I8>
 __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, GemmA a,
                                                          const void* __restrict__ W,
                                                          int64_t ldw, EpiParams e,
-                                                         int a_bytes, int w_bytes, int group_m,
-                                                         int remap) {
+                                                         int group_m, int remap) {
   // The buffer-resource builtins exist only for the device; the host pass
   // needs nothing but this kernel's launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -786,12 +795,27 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   const int tn = (pid % width) / gsz;
   const int bm0 = tm * C::BM, bn0 = tn * C::BN;
 
-  const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.ptr), (short)0, a_bytes,
-                                                    0x00020000);
-  const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(W), (short)0, w_bytes,
-                                                    0x00020000);
   constexpr int ES = I8 ? 1 : 2;            // bytes per element
   constexpr int BKE = C::ROWB / ES;         // K elements per step
+
+  // The buffer descriptors start at this tile's first A row and first W
+  // row and cover exactly the rows the tile reads (rows past M or N are
+  // clamped to the last one), so a descriptor's 32-bit extent never limits
+  // the operand sizes: one tile spans at most BM rows (plus one batch
+  // stride where a tile crosses a batch item of the conv windows).
+  auto a_elem = [&](int m) -> int64_t {
+    const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+    return (int64_t)b * a.batch_stride + (int64_t)t * a.lda;
+  };
+  const int64_t a_row0 = a_elem(bm0);
+  const int64_t a_span = a_elem(min(bm0 + C::BM, M) - 1) - a_row0 + K;
+  const int64_t w_span = (int64_t)(min(bn0 + C::BN, N) - 1 - bn0) * ldw + K;
+  const auto ra = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(static_cast<const char*>(a.ptr)) + a_row0 * ES, (short)0,
+      (int)(a_span * ES), 0x00020000);
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(static_cast<const char*>(W)) + (int64_t)bn0 * ldw * ES, (short)0,
+      (int)(w_span * ES), 0x00020000);
 
   // lane -> tile row within its DMA block and the logical chunk that belongs
   // in its slot (lane % CPR) under the swizzle
@@ -803,8 +827,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     const int lchunk = (lane % C::CPR) ^ ((row / C::RPW) % C::CPR);
     int m = bm0 + row;
     m = m < M ? m : M - 1;
-    const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
-    aoff[j] = (uint32_t)(((int64_t)b * a.batch_stride + (int64_t)t * a.lda) * ES + lchunk * 16);
+    aoff[j] = (uint32_t)((a_elem(m) - a_row0) * ES + lchunk * 16);
   }
 #pragma unroll
   for (int j = 0; j < C::B_INSTR; ++j) {
@@ -812,7 +835,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     const int lchunk = (lane % C::CPR) ^ ((row / C::RPW) % C::CPR);
     int n = bn0 + row;
     n = n < N ? n : N - 1;
-    boff[j] = (uint32_t)((int64_t)n * ldw * ES + lchunk * 16);
+    boff[j] = (uint32_t)((int64_t)(n - bn0) * ldw * ES + lchunk * 16);
   }
   auto issue = [&](int kt) {
     uint8_t* base = smem + (kt % C::S) * C::STAGE;
@@ -1038,8 +1061,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
 
 template <class C, bool I8 = false>
 static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const void* W,
-                                  int64_t ldw, int mode, const EpiParams& e,
-                                  int a_bytes, int w_bytes, hipStream_t s) {
+                                  int64_t ldw, int mode, const EpiParams& e, hipStream_t s) {
   const int tiles = ((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
   dim3 grid(tiles * e.splits), block(C::NT);
   // Tile order. Workgroups go to the 8 XCDs round-robin by id; with
@@ -1050,22 +1072,16 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const voi
   // fc1 shape this halves the Infinity Cache / HBM reads (1.41 -> 0.76 GB)
   // and takes 5 % off the time; for the 256x256 tile (one workgroup per CU)
   // the plain grouped order measured as good.
-  int group_m = C::BM == 128 ? 8 : kGroupM, remap = C::BM == 128 ? 1 : 0;
-  // WXH_GEMM_MAP="remap,group" overrides the tile order (tuning sweeps)
-  if (const char* m = getenv("WXH_GEMM_MAP")) {
-    int r = 0, g = 0;
-    if (sscanf(m, "%d,%d", &r, &g) == 2 && g > 0) {
-      remap = r;
-      group_m = g;
-    }
-  }
+  const int group_m = C::BM == 128 ? 8 : kGroupM, remap = C::BM == 128 ? 1 : 0;
 #define WX_DMA(MD)                                                                   \
   case MD:                                                                           \
-    gemm_dma_kernel<C, MD, I8><<<grid, block, 0, s>>>(M, N, K, a, W, ldw, e, a_bytes, \
-                                                      w_bytes, group_m, remap);      \
+    gemm_dma_kernel<C, MD, I8><<<grid, block, 0, s>>>(M, N, K, a, W, ldw, e, group_m, \
+                                                      remap);                        \
     break;
   if (mode == EPI_BF16 && e.gelu == GELU_ERF) mode = EPI_BF16_GELU;
   if (mode == EPI_BF16 && e.gelu == GELU_POLY4_RNE) mode = EPI_BF16_POLY4;
+  if (mode == EPI_CONV1 && e.gelu == GELU_POLY4_RNE) mode = EPI_CONV1_POLY4;
+  if (mode == EPI_CONV2 && e.gelu == GELU_POLY4_RNE) mode = EPI_CONV2_POLY4;
   if constexpr (I8) {
     // the int8 encoder's and the C ABI's epilogues
     switch (mode) {
@@ -1078,6 +1094,7 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const voi
     switch (mode) {
       WX_DMA(EPI_F32) WX_DMA(EPI_BF16) WX_DMA(EPI_RESID) WX_DMA(EPI_CONV1)
       WX_DMA(EPI_CONV2) WX_DMA(EPI_QKV) WX_DMA(EPI_BF16_GELU) WX_DMA(EPI_BF16_POLY4)
+      WX_DMA(EPI_CONV1_POLY4) WX_DMA(EPI_CONV2_POLY4)
       default:
         return hipErrorInvalidValue;
     }
@@ -1086,19 +1103,18 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const voi
   return hipGetLastError();
 }
 
-// Byte extent of A that rows [0, M) can touch (the buffer descriptor's
-// range); the largest row offset is that of the last row of the last batch
-// item or of the first batch item's last row.
-static int64_t a_extent_bytes(int M, int K, const GemmA& a, int es = 2) {
-  auto off = [&](int m) {
-    const int b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
-    return (int64_t)b * a.batch_stride + (int64_t)t * a.lda;
-  };
-  const int last_first = (M < a.rows_per_batch ? M : a.rows_per_batch) - 1;
-  int64_t hi = off(M - 1);
-  const int64_t h2 = off(last_first);
-  if (h2 > hi) hi = h2;
-  return (hi + K) * es;
+// Whether one tile's operand rows fit a buffer descriptor (32-bit byte
+// extent, measured from the tile's first row): at most `rows` rows of A,
+// which may cross one batch item of the conv windows, and of W. The
+// kernel takes A's row offsets as rising with the row index, which holds
+// when every batch item's rows end before the next item starts.
+static bool tile_extents_fit(int rows, int M, int K, const GemmA& a, int64_t ldw, int es) {
+  const bool rising = a.rows_per_batch >= M ||
+                      a.batch_stride >= (int64_t)(a.rows_per_batch - 1) * a.lda + K;
+  if (!rising) return false;
+  const int64_t a_span = (int64_t)rows * a.lda + a.batch_stride + K;
+  const int64_t w_span = (int64_t)rows * ldw + K;
+  return a_span * es < (1ll << 31) && w_span * es < (1ll << 31);
 }
 
 // Split count for a launch of `tiles` 128x128 tiles at one workgroup per
@@ -1106,21 +1122,22 @@ static int64_t a_extent_bytes(int M, int K, const GemmA& a, int es = 2) {
 // 64-multiple pieces that keeps tiles x splits within the 256 CUs and each
 // piece at least 1536 long. Shorter pieces lose more to writing and reading
 // the partials than they gain (measured at batch 1: fc2, K 5120, 2 splits
-// 74 -> 47 us; out-proj, K 1280, 2 splits slower). WXH_GEMM_SPLITK=n
-// forces n (tuning sweeps; 1 disables).
+// 74 -> 47 us; out-proj, K 1280, 2 splits slower). e.force_splits (the
+// context's tuning switch) overrides: 1 never splits, n splits n ways.
 static int pick_splits(int M, int N, int K, int64_t tiles, const EpiParams& e) {
   if (!e.sk_ws || !e.sk_cnt || tiles > e.sk_cnt_len) return 1;
   auto fits = [&](int sp) {
     return K % (sp * 64) == 0 && (int64_t)sp * M * N <= e.sk_ws_elems;
   };
-  if (const char* f = getenv("WXH_GEMM_SPLITK")) {
-    const int sp = atoi(f);
-    return sp > 1 && fits(sp) ? sp : 1;
-  }
+  if (e.force_splits > 0) return e.force_splits > 1 && fits(e.force_splits) ? e.force_splits : 1;
   for (int sp = 4; sp >= 2; --sp)
     if (tiles * sp <= 256 && K / sp >= 1536 && fits(sp)) return sp;
   return 1;
 }
+
+using T128 = DCfg<128, 128, 2, 2, 64, 2>;
+using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
+using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
 
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
                        int64_t ldw, int mode, const EpiParams& e_in,
@@ -1128,56 +1145,28 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   if (M <= 0 || N <= 0) return hipSuccess;
   EpiParams e = e_in;
   e.splits = 1;
-  const int64_t ab = a_extent_bytes(M, K, a);
-  const int64_t wb = ((int64_t)(N - 1) * ldw + K) * 2;
   const bool dma = K > 0 && K % 64 == 0 && a.lda % 8 == 0 && ldw % 8 == 0 &&
                    a.batch_stride % 8 == 0 && ((uintptr_t)a.ptr & 15) == 0 &&
-                   ((uintptr_t)W & 15) == 0 && ab < (1ll << 31) && wb < (1ll << 31);
-  // WXH_GEMM_TILE overrides the tile choice (tuning sweeps)
-  const char* force = getenv("WXH_GEMM_TILE");
-  const std::string f = force ? force : "";
-  if (!dma || f == "v1") return gemm_launch_cfg<Cfg128>(M, N, K, a, W, ldw, mode, e, s);
-  using T128 = DCfg<128, 128, 2, 2, 64, 2>;
-  using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
-  // deeper rings (BK 32, 4 slots), kept for comparison: on MI355X they move
-  // the same bytes in the same time as the 2-slot BK 64 ring
-  using T128k32s4 = DCfg<128, 128, 2, 2, 32, 4>;
-  using T256w8k32s4 = DCfg<256, 256, 2, 4, 32, 4>;
-  using T128s3 = DCfg<128, 128, 2, 2, 64, 3>;
-  using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
-  using T128s4 = DCfg<128, 128, 2, 2, 64, 4>;
-  const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-#define WX_TRY(NAME, CFG)                                                              \
-  if (f == NAME) {                                                                     \
-    if (K % CFG::BK) return hipErrorInvalidValue;                                      \
-    if (CFG::BM == 128) e.splits = pick_splits(M, N, K, tiles128, e);                  \
-    return gemm_dma_launch<CFG>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);     \
-  }
-  WX_TRY("128x128", T128)
-  WX_TRY("128x128s3", T128s3)
-  WX_TRY("128x128s4", T128s4)
-  WX_TRY("256x256w8", T256w8)
-  WX_TRY("128x128k32s4", T128k32s4)
-  WX_TRY("256x256w8k32s4", T256w8k32s4)
-#undef WX_TRY
+                   ((uintptr_t)W & 15) == 0 && tile_extents_fit(256, M, K, a, ldw, 2);
+  if (!dma) return gemm_launch_cfg<Cfg128>(M, N, K, a, W, ldw, mode, e, s);
   // Measured on MI355X over the encoder shapes with random operands: the
   // 8-wave 256x256 tile (128x64 per wave, 2 waves per SIMD, one workgroup per
   // CU) is fastest once there are enough tiles to fill the 256 CUs (batch 16:
   // fc1 367 us vs 399 for 128x128, QKV 269 vs 295, fc2 319 vs 370). Below
   // that (batch 1) the 128x128 tile keeps more CUs busy.
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-  if (big_tiles >= 256)
-    return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  if (big_tiles >= 256) return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, s);
   // At most one 128x128 tile per CU (batch 1-2: fc2, out-proj, conv2), the
   // per-step time is the DMA latency: a 3-slot ring (one workgroup per CU)
   // keeps two steps in flight (batch 1: fc2 74 -> 54 us, out-proj 27 -> 24),
   // and split-K adds workgroups where K is long. With more tiles, two
   // workgroups per CU on the 2-slot ring do better (batch 1 QKV 29 vs 37 us).
+  const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
   if (tiles128 <= 256) {
     e.splits = pick_splits(M, N, K, tiles128, e);
-    return gemm_dma_launch<T128w8s3>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+    return gemm_dma_launch<T128w8s3>(M, N, K, a, W, ldw, mode, e, s);
   }
-  return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, s);
 }
 
 // Same tile choice as launch_gemm (the K-step covers 128 int8 elements, the
@@ -1188,22 +1177,15 @@ hipError_t launch_gemm_i8(int M, int N, int K, const GemmA& a, const int8_t* W, 
   if (M <= 0 || N <= 0) return hipSuccess;
   EpiParams e = e_in;
   e.splits = 1;
-  const int64_t ab = a_extent_bytes(M, K, a, 1);
-  const int64_t wb = (int64_t)(N - 1) * ldw + K;
   if (K <= 0 || K % kI8KAlign || a.lda % 16 || ldw % 16 || a.batch_stride % 16 ||
-      ((uintptr_t)a.ptr & 15) || ((uintptr_t)W & 15) || ab >= (1ll << 31) ||
-      wb >= (1ll << 31) || !e.a_scale || !e.w_scale)
+      ((uintptr_t)a.ptr & 15) || ((uintptr_t)W & 15) || !tile_extents_fit(256, M, K, a, ldw, 1) ||
+      !e.a_scale || !e.w_scale)
     return hipErrorInvalidValue;
-  using T128 = DCfg<128, 128, 2, 2, 64, 2>;
-  using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
-  using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
   const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-  if (big_tiles >= 256)
-    return gemm_dma_launch<T256w8, true>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
-  if (tiles128 <= 256)
-    return gemm_dma_launch<T128w8s3, true>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
-  return gemm_dma_launch<T128, true>(M, N, K, a, W, ldw, mode, e, (int)ab, (int)wb, s);
+  if (big_tiles >= 256) return gemm_dma_launch<T256w8, true>(M, N, K, a, W, ldw, mode, e, s);
+  if (tiles128 <= 256) return gemm_dma_launch<T128w8s3, true>(M, N, K, a, W, ldw, mode, e, s);
+  return gemm_dma_launch<T128, true>(M, N, K, a, W, ldw, mode, e, s);
 }
 
 }  // namespace wx

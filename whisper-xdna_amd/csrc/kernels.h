@@ -65,7 +65,14 @@ enum EpiMode {
   EPI_BF16_GELU = 6,   // out bf16 = gelu_erf(acc + bias)
   EPI_BF16_POLY4 = 7,  // out bf16 = poly4 GELU (g4f) of acc + bias
   EPI_F32_GELU = 8,    // out fp32 = gelu_erf(acc + bias)
+  // EPI_CONV1 / EPI_CONV2 with the poly4 GELU (g4f) in place of erf, chosen
+  // by launch_gemm from EpiParams::gelu == GELU_POLY4_RNE
+  EPI_CONV1_POLY4 = 9,
+  EPI_CONV2_POLY4 = 10,
 };
+
+constexpr bool epi_conv1(int m) { return m == EPI_CONV1 || m == EPI_CONV1_POLY4; }
+constexpr bool epi_conv2(int m) { return m == EPI_CONV2 || m == EPI_CONV2_POLY4; }
 
 struct GemmA {
   const void* ptr;  // bf16 (launch_gemm) or int8 (launch_gemm_i8) elements
@@ -81,7 +88,7 @@ struct EpiParams {
   const float* aux = nullptr;      // positional embedding [T, N] (EPI_CONV2)
   int rows_per_batch = 1;          // T: rows of one batch item
   int64_t out_batch_stride = 0;    // EPI_CONV1: elements per padded batch item
-  int gelu = GELU_NONE;            // EPI_BF16 activation
+  int gelu = GELU_NONE;            // EPI_BF16 activation; EPI_CONV*: erf unless POLY4_RNE
   uint16_t* q = nullptr;           // EPI_QKV destinations
   uint16_t* k = nullptr;
   uint16_t* vt = nullptr;
@@ -101,6 +108,7 @@ struct EpiParams {
   int64_t sk_ws_elems = 0;
   unsigned* sk_cnt = nullptr;
   int sk_cnt_len = 0;
+  int force_splits = 0;            // 0: automatic; 1: never split; n: n splits where K allows
   int splits = 1;                  // set by launch_gemm
   // launch_gemm_i8: acc (int32) becomes (float(acc) * a_scale[row]) *
   // w_scale[col] before the bias and the epilogue
@@ -161,10 +169,12 @@ __host__ __device__ inline int vt_key(int t) {
 // bf16 or fp32 per o_dtype. With q_prescaled, Q already holds
 // bf16(q * scale * log2(e)) (attn_q_scale), written so by the QKV GEMM's
 // epilogue, and `scale` is not used.
+// keysplit: 0 splits a workgroup's keys over two wave groups when there
+// are fewer workgroups than CUs, 1 never does.
 hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
                             const uint16_t* Vt, int batch, int n_head, int T,
                             float scale, void* O, int o_dtype, int64_t ldo,
-                            hipStream_t s, bool q_prescaled = false);
+                            hipStream_t s, bool q_prescaled = false, int keysplit = 0);
 
 // The factor a pre-scaled Q carries: the softmax scale times log2(e), so
 // that a score leaves the MFMA in the exp2 domain.

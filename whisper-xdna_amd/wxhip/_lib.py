@@ -12,16 +12,17 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libwxhip.so")
 
 WXH_OK, WXH_ERR_INVALID, WXH_ERR_HIP, WXH_ERR_INJECTED = 0, 1, 2, 3
-WXH_ERR_UNSUPPORTED, WXH_ERR_STATE = 4, 5
+WXH_ERR_UNSUPPORTED, WXH_ERR_STATE, WXH_ERR_TIMEOUT = 4, 5, 6
 WXH_BF16, WXH_F32, WXH_I8 = 0, 1, 2
 WXH_GELU_ERF, WXH_GELU_POLY4_RNE, WXH_GELU_POLY4_TRUNC = 0, 1, 2
 WXH_EPI_F32, WXH_EPI_BF16, WXH_EPI_BF16_GELU_ERF = 0, 1, 2
 WXH_EPI_BF16_GELU_POLY4, WXH_EPI_RESID_F32, WXH_EPI_F32_GELU_ERF = 3, 4, 5
 WXH_FAIL_GEMM, WXH_FAIL_ATTN, WXH_FAIL_ROWOP, WXH_FAIL_ENCODER = 1, 2, 4, 8
 WXH_FAIL_FRONTEND = 16
+WXH_TUNE_GEMM_SPLITK, WXH_TUNE_ATTN_KEYSPLIT = 0, 1
 
 ERROR_NAMES = {1: "invalid argument", 2: "HIP error", 3: "injected failure",
-               4: "unsupported", 5: "bad state"}
+               4: "unsupported", 5: "bad state", 6: "deadline passed"}
 
 
 class WxhLibraryError(RuntimeError):
@@ -38,7 +39,8 @@ class WxhError(RuntimeError):
 
 class EncoderDims(C.Structure):
     _fields_ = [("n_mels", C.c_int), ("d_model", C.c_int), ("n_head", C.c_int),
-                ("n_layer", C.c_int), ("n_ctx", C.c_int), ("mlp_gelu", C.c_int)]
+                ("n_layer", C.c_int), ("n_ctx", C.c_int), ("mlp_gelu", C.c_int),
+                ("conv_gelu", C.c_int)]
 
 
 P, I, I64, F, U32 = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_uint32
@@ -53,6 +55,8 @@ SIGNATURES = {
     "wxh_set_fail_inject": [P, U32],
     "wxh_get_stream": [P, PP],
     "wxh_synchronize": [P],
+    "wxh_set_timeout": [P, I],
+    "wxh_set_tuning": [P, I, I],
     "wxh_log_mel": [P, P, I, I, I, P, P],
     "wxh_mel_filterbank": [I, P],
     "wxh_layernorm": [P, P, I, I64, P, I64, P, I64, P, P, F, P, I, I64, I, I, P],

@@ -1,15 +1,13 @@
-"""Audio input and the log-mel front end, with the names the reference uses.
+"""The log-mel front end, with the names the reference calls.
 
-The reference reads 16-bit PCM WAV through src/audio_io.py (``pcm16_mono``,
-``read_wav``) and turns it into encoder input with openai-whisper's
+The reference turns 16 kHz samples into encoder input with openai-whisper's
 ``pad_or_trim`` + ``log_mel_spectrogram`` on the CPU (tools/dump_ref.py:55-57,
-serve/npu_stt_server.py:334-336). Here the same functions exist with the
-same arguments; ``log_mel_spectrogram`` runs on the GPU (``wxh_log_mel``) and
-returns a device tensor, ready for ``HipEncoder.forward``.
+serve/npu_stt_server.py:334-336). Here the same two functions take the same
+arguments; ``log_mel_spectrogram`` runs on the GPU (``wxh_log_mel``) and
+returns a device tensor, ready for ``HipEncoder.forward``. Decoding audio
+files (the reference's src/audio_io.py) is outside this path: callers pass
+samples.
 """
-import io
-import wave
-
 import numpy as np
 
 SAMPLE_RATE = 16000
@@ -20,31 +18,6 @@ N_SAMPLES = CHUNK_LENGTH * SAMPLE_RATE   # 480000 samples in a 30 s window
 N_FRAMES = N_SAMPLES // HOP_LENGTH      # 3000 mel frames
 
 _dev = None
-
-
-def pcm16_mono(raw, expect_sr=SAMPLE_RATE):
-    """Decode WAV bytes to float32 in [-1, 1), channels averaged. Raises
-    ValueError on anything but 16-bit PCM at `expect_sr` (src/audio_io.py:15-32)."""
-    with wave.open(io.BytesIO(raw), "rb") as w:
-        nch, sw, sr, n = w.getnchannels(), w.getsampwidth(), w.getframerate(), w.getnframes()
-        frames = w.readframes(n)
-    if sw != 2:
-        raise ValueError(f"expected 16-bit PCM, got sampwidth={sw}")
-    if expect_sr and sr != expect_sr:
-        raise ValueError(f"expected {expect_sr} Hz, got {sr}")
-    a = np.frombuffer(frames, dtype="<i2").astype(np.float32) / 32768.0
-    if nch > 1:
-        a = a.reshape(-1, nch).mean(axis=1)
-    return a, sr, nch
-
-
-def read_wav(path, expect_sr=SAMPLE_RATE, verbose=True):
-    """Same, from a file (src/audio_io.py:35-44)."""
-    with open(path, "rb") as f:
-        a, sr, nch = pcm16_mono(f.read(), expect_sr)
-    if verbose:
-        print(f"wav: sr={sr} ch={nch} samples={len(a)} dur={len(a) / sr:.2f}s", flush=True)
-    return a
 
 
 def pad_or_trim(array, length=N_SAMPLES, axis=-1):
@@ -73,8 +46,8 @@ def pad_or_trim(array, length=N_SAMPLES, axis=-1):
 def log_mel_spectrogram(audio, n_mels=80, padding=0, device=None):
     """Whisper's log-mel features on the GPU.
 
-    audio: a WAV path, or fp32 samples at 16 kHz ([n] or [B, n]; numpy or
-    torch, any device); `padding` zero samples are appended first. Returns
+    audio: fp32 samples at 16 kHz ([n] or [B, n]; numpy or torch, any
+    device); `padding` zero samples are appended first. Returns
     an fp32 torch tensor on the GPU, [n_mels, n // 160] (or [B, n_mels,
     n // 160]), each clip floored at its own maximum - 8.
     """
@@ -86,8 +59,9 @@ def log_mel_spectrogram(audio, n_mels=80, padding=0, device=None):
         if _dev is None:
             _dev = Device(0)
         dev = _dev
-    if isinstance(audio, str):
-        audio = read_wav(audio, verbose=False)
+    if isinstance(audio, (str, bytes)):
+        raise TypeError("log_mel_spectrogram takes samples; decoding audio files is "
+                        "outside this path")
     if not torch.is_tensor(audio):
         audio = torch.from_numpy(np.ascontiguousarray(audio, dtype=np.float32))
     audio = audio.to(device=dev.device, dtype=torch.float32)

@@ -55,6 +55,19 @@ class Device:
     def set_fail_inject(self, mask):
         L.call("wxh_set_fail_inject", self._h, mask)
 
+    def set_timeout(self, ms):
+        """Deadline of the library's own blocking waits (0: none); see
+        wxh_set_timeout."""
+        L.call("wxh_set_timeout", self._h, int(ms))
+
+    def set_tuning(self, what, value):
+        """A tuning switch (WXH_TUNE_*; 0 = automatic); see wxh_set_tuning."""
+        L.call("wxh_set_tuning", self._h, int(what), int(value))
+
+    def wait(self):
+        """wxh_synchronize: the context's stream, under its deadline."""
+        L.call("wxh_synchronize", self._h)
+
     def close(self):
         if getattr(self, "_h", None):
             self.lib.wxh_destroy(self._h)

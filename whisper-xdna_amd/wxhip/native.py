@@ -43,17 +43,20 @@ def weight_names(n_layer):
 class HipEncoder:
     """Whisper encoder on one GPU: weights resident, forward as a hipGraph."""
 
-    def __init__(self, dev, W, n_layer=None, mlp_gelu="erf", graph=True, int8=False):
+    def __init__(self, dev, W, n_layer=None, mlp_gelu="erf", graph=True, int8=False,
+                 conv_gelu="erf"):
         n_mels, d, n_head, nl, n_ctx = geometry(W)
         self.dev = dev
         self.n_mels, self.d_model, self.n_head, self.n_ctx = n_mels, d, n_head, n_ctx
         self.n_layer = nl if n_layer is None else n_layer
         if not 0 <= self.n_layer <= nl:
             raise ValueError(f"n_layer={self.n_layer} but the weights have {nl} blocks")
-        if mlp_gelu not in _GELU:
-            raise ValueError(f"mlp_gelu must be one of {sorted(_GELU)}")
-        self.mlp_gelu = mlp_gelu
-        dims = L.EncoderDims(n_mels, d, n_head, self.n_layer, n_ctx, _GELU[mlp_gelu])
+        for name, v in (("mlp_gelu", mlp_gelu), ("conv_gelu", conv_gelu)):
+            if v not in _GELU:
+                raise ValueError(f"{name} must be one of {sorted(_GELU)}")
+        self.mlp_gelu, self.conv_gelu = mlp_gelu, conv_gelu
+        dims = L.EncoderDims(n_mels, d, n_head, self.n_layer, n_ctx, _GELU[mlp_gelu],
+                             _GELU[conv_gelu])
         h = C.c_void_p()
         L.call("wxh_encoder_create", dev.handle, C.byref(dims), C.byref(h))
         self._h = h
