@@ -141,6 +141,20 @@ int wxh_set_tuning(wxh_ctx* ctx, int what, int value);
 int wxh_log_mel(wxh_ctx* ctx, const float* audio, int batch, int n_samples, int n_mels,
                 float* out, void* stream);
 
+/* wxh_log_mel without any device allocation, for callers that cannot
+ * allocate (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). It has no counterpart in the reference. Same arguments,
+ * kernels and results as wxh_log_mel; the clip-maximum scratch and the
+ * filterbank constants live in a fixed device array the library holds on
+ * each GPU (96 KiB, resolved and filled once per device by wxh_create).
+ * Limits: batch <= 256 clips (WXH_ERR_INVALID beyond), n_mels 80 or 128
+ * (WXH_ERR_UNSUPPORTED otherwise). Every call on one GPU shares that array
+ * (the slots are re-initialised by each call): calls that overlap in time on
+ * one GPU, from any context or stream, race. Fail-inject bit
+ * WXH_FAIL_FRONTEND. */
+int wxh_log_mel_noalloc(wxh_ctx* ctx, const float* audio, int batch, int n_samples,
+                        int n_mels, float* out, void* stream);
+
 /* Host-side: the mel filterbank wxh_log_mel applies, [n_mels][201] float32
  * into `out` (host memory), as librosa.filters.mel(16000, 400, n_mels)
  * builds it. Needs no GPU. */

@@ -20,6 +20,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -202,6 +203,58 @@ hipError_t launch_log_mel(const float* audio, int batch, int n_samples, int n_me
   const int chunks = (int)std::min<int64_t>((per_clip + 2047) / 2048, 1024);
   logmel_norm_kernel<<<dim3(chunks, batch), 256, 0, s>>>(out, per_clip, slots);
   return hipGetLastError();
+}
+
+// ------------------------------------------------------------ allocation-free
+// Everything launch_log_mel needs beyond its input and output, for callers
+// that cannot allocate device memory, in one file-scope device array: the
+// clip-maximum slots of up to kNoAllocClips clips, then the constants of the
+// two filterbanks Whisper uses (80 and 128 mels). Each GPU the library runs
+// on holds its own copy, 96 KiB, until the process ends. In host code
+// `scratch` only names the symbol: its device address on each GPU comes from
+// hipGetSymbolAddress, once per device at set-up, and only that address is
+// ever handed to a kernel.
+constexpr int kNoAllocConstBytes = 16 << 10;
+constexpr int kNoAllocSlotBytes = kNoAllocClips * kMaxSlots * (int)sizeof(int);
+constexpr int kNoAllocMels[2] = {80, 128};
+static __device__ __align__(256) uint8_t scratch[kNoAllocSlotBytes + 2 * kNoAllocConstBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[kMaxDevices] = {};  // per device: the address of `scratch` there
+}  // namespace
+
+hipError_t logmel_noalloc_setup(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  if (g_scratch[device]) return hipSuccess;
+  void* base = nullptr;
+  hipError_t e = hipGetSymbolAddress(&base, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  for (int i = 0; i < 2; ++i) {
+    const std::vector<uint8_t> c = logmel_constants(kNoAllocMels[i]);
+    if (c.size() > (size_t)kNoAllocConstBytes) return hipErrorInvalidValue;
+    e = hipMemcpy(static_cast<uint8_t*>(base) + kNoAllocSlotBytes + i * kNoAllocConstBytes,
+                  c.data(), c.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return e;
+  }
+  g_scratch[device] = static_cast<uint8_t*>(base);
+  return hipSuccess;
+}
+
+hipError_t launch_log_mel_noalloc(int device, const float* audio, int batch, int n_samples,
+                                  int n_mels, float* out, hipStream_t s) {
+  uint8_t* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device >= 0 && device < kMaxDevices) base = g_scratch[device];
+  }
+  const int which = n_mels == kNoAllocMels[0] ? 0 : n_mels == kNoAllocMels[1] ? 1 : -1;
+  if (!base || which < 0 || batch > kNoAllocClips) return hipErrorInvalidValue;
+  return launch_log_mel(audio, batch, n_samples, n_mels,
+                        base + kNoAllocSlotBytes + which * kNoAllocConstBytes, out,
+                        reinterpret_cast<int*>(base), s);
 }
 
 }  // namespace wx

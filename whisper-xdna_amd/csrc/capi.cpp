@@ -155,10 +155,13 @@ int wxh_create(int device, wxh_ctx** out) {
   }
   e = wx::init_rowop_tables(c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  // the allocation-free front end's device array: its address on this
+  // device and its filterbank constants, once per device
+  if (e == hipSuccess) e = wx::logmel_noalloc_setup(device);
   if (e != hipSuccess) {
     (void)hipStreamDestroy(c->stream);
     delete c;
-    return fail(WXH_ERR_HIP, "wxh_create: row-kernel tables: %s", hipGetErrorString(e));
+    return fail(WXH_ERR_HIP, "wxh_create: device tables: %s", hipGetErrorString(e));
   }
   *out = c;
   return WXH_OK;
@@ -322,6 +325,24 @@ int wxh_log_mel(wxh_ctx* c, const float* audio, int batch, int n_samples, int n_
   }
   WXH_HIP(wx::launch_log_mel(audio, batch, n_samples, n_mels, it->second, out,
                              c->logmel_slots, pick(c, stream)));
+  return WXH_OK;
+}
+
+int wxh_log_mel_noalloc(wxh_ctx* c, const float* audio, int batch, int n_samples,
+                        int n_mels, float* out, void* stream) {
+  if (int r = check_ctx(c, WXH_FAIL_FRONTEND, "wxh_log_mel_noalloc")) return r;
+  WXH_REQUIRE(audio && out, "wxh_log_mel_noalloc: null pointer");
+  WXH_REQUIRE(batch >= 0 && n_samples >= 400, "wxh_log_mel_noalloc: batch=%d n_samples=%d",
+              batch, n_samples);
+  WXH_REQUIRE(batch <= wx::kNoAllocClips,
+              "wxh_log_mel_noalloc: batch=%d is more clips than its fixed scratch holds (%d)",
+              batch, wx::kNoAllocClips);
+  if (n_mels != 80 && n_mels != 128)
+    return fail(WXH_ERR_UNSUPPORTED,
+                "wxh_log_mel_noalloc: n_mels=%d; its fixed scratch holds the 80- and 128-mel "
+                "filterbanks only (wxh_log_mel takes any)", n_mels);
+  WXH_HIP(wx::launch_log_mel_noalloc(c->device, audio, batch, n_samples, n_mels, out,
+                                     pick(c, stream)));
   return WXH_OK;
 }
 

@@ -197,6 +197,15 @@ std::vector<uint8_t> logmel_constants(int n_mels);
 std::vector<float> mel_filterbank(int n_mels);
 hipError_t launch_log_mel(const float* audio, int batch, int n_samples, int n_mels,
                           const uint8_t* consts, float* out, int* slots, hipStream_t s);
+// The same on the device's file-scope scratch array (no allocation): set up
+// once per device (that device current) by logmel_noalloc_setup, which
+// resolves the array's address there and writes the 80- and 128-mel
+// constants into it; then n_mels must be 80 or 128 and batch <=
+// kNoAllocClips. Calls on one device share the array.
+constexpr int kNoAllocClips = 256;
+hipError_t logmel_noalloc_setup(int device);
+hipError_t launch_log_mel_noalloc(int device, const float* audio, int batch, int n_samples,
+                                  int n_mels, float* out, hipStream_t s);
 
 hipError_t launch_prep_mel(const float* mel, int batch, int C, int T,
                            uint16_t* out, hipStream_t s);

@@ -58,6 +58,7 @@ SIGNATURES = {
     "wxh_set_timeout": [P, I],
     "wxh_set_tuning": [P, I, I],
     "wxh_log_mel": [P, P, I, I, I, P, P],
+    "wxh_log_mel_noalloc": [P, P, I, I, I, P, P],
     "wxh_mel_filterbank": [I, P],
     "wxh_layernorm": [P, P, I, I64, P, I64, P, I64, P, P, F, P, I, I64, I, I, P],
     "wxh_gelu": [P, P, I, I64, P, I64, I, I, I, P],
