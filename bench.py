@@ -30,7 +30,9 @@ readings into bytes. KERNEL: fc1 (erf-GELU epilogue, bf16 out), fc2 and
 out_proj (fp32 residual epilogue), qkv (the QKV main loop with a plain bf16
 epilogue), attention (softmax(Q K^T / 8) V over B*20 heads of 1500 keys),
 rowops (LayerNorm [1500,1280] bf16 and [24000,1280] fp32 -> bf16, erf- and
-poly4-GELU [1500,5120], softmax [30000,1500], each N times).
+poly4-GELU [1500,5120], softmax [30000,1500], each N times), encoder (graph
+replays of the whole 32-layer forward at batch B: every kernel as the
+encoder launches it, split-K included).
 """
 import argparse
 import json
@@ -137,7 +139,7 @@ def latency_median(enc, mel, n, warmup):
     return float(np.median([a.elapsed_time(b) for a, b in evs])) / 1e3
 
 
-PROBE_KERNELS = ("fc1", "fc2", "qkv", "out_proj", "attention", "rowops")
+PROBE_KERNELS = ("fc1", "fc2", "qkv", "out_proj", "attention", "rowops", "encoder")
 
 
 def probe(kernel, reps, batch):
@@ -170,6 +172,12 @@ def probe(kernel, reps, batch):
         else:
             x = normal((M, N), 1.0, torch.float32)
             cases = [(kernel, lambda: dev.gemm(A, W, b, L.WXH_EPI_RESID_F32, out=x))]
+    elif kernel == "encoder":
+        from wxhip import synth
+        enc = wxhip.HipEncoder(dev, synth.make_weights("large-v3"))
+        mel = torch.from_numpy(synth.make_mel_batch(batch, 128, 3000)).to(dev.device)
+        enc.forward(mel)            # graph captured outside the counted phase
+        cases = [("encoder forward (graph replay)", lambda: enc.forward(mel))]
     elif kernel == "attention":
         Q, Kt, Vt = dev.attn_buffers(batch, NH, CTX)
         for t in (Q, Kt, Vt):

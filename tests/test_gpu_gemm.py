@@ -173,3 +173,34 @@ def test_hiprt_matmul_plugin(dev):
     assert rt.calls == 1
     out2 = rt.matmul(A, B, bias=bias)
     np.testing.assert_array_equal(out, out2)
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(4096 + 100, 4096, 3072, "resid"),
+                                       (4096, 4096 + 64, 4096, "bf16"),
+                                       (4200, 4096, 3072 + 64, "f32")])
+def test_gemm_long_k_asymmetric_ring(dev, M, N, K, epi):
+    """At least 256 tiles of 256x256 with K >= 3072 take the ring where A has
+    three LDS slots and W two (the batch-16 fc2 kernel); partial edge tiles
+    and a K-step count that is not a multiple of 3 included. A sample of
+    rows and columns against the fp64 product of the same bf16 operands."""
+    case(f"gemm asymmetric ring M={M} N={N} K={K} {epi}")
+    A, W, b = _operands(M, N, K, seed=K + N)
+    rows = np.r_[0:64, M // 2:M // 2 + 64, M - 64:M]
+    cols = np.r_[0:64, N // 2 - 32:N // 2 + 32, N - 64:N]
+    ref, mag = _exact(A[rows], W[cols], b[cols])
+    Ad, Wd, bd = _dev(A, dev), _dev(W, dev), _dev(b, dev, False)
+    if epi == "resid":
+        x = np.random.default_rng(1).normal(0, 1, (M, N)).astype(np.float32)
+        C = dev.gemm(Ad, Wd, bd, L.WXH_EPI_RESID_F32, out=_dev(x, dev, False))
+        got = C.cpu().numpy()[np.ix_(rows, cols)] - x[np.ix_(rows, cols)]
+        tol = 2e-4 * mag + 1e-6 + 2.0 ** -22 * np.abs(x[np.ix_(rows, cols)])
+    elif epi == "bf16":
+        C = dev.gemm(Ad, Wd, bd, L.WXH_EPI_BF16)
+        got = OB.to_f32(bits(C))[np.ix_(rows, cols)]
+        tol = 2e-4 * mag + 1e-6 + 2.0 ** -8 * np.abs(ref)   # one bf16 rounding
+    else:
+        C = dev.gemm(Ad, Wd, bd, L.WXH_EPI_F32)
+        got = C.cpu().numpy()[np.ix_(rows, cols)]
+        tol = 2e-4 * mag + 1e-6
+    err = np.abs(got - ref)
+    assert (err <= tol).all(), f"{int((err > tol).sum())} off, max err {err.max()}"

@@ -485,9 +485,14 @@ using Cfg128 = Cfg<128, 128, 64, 2, 2>;
 // in slot c ^ ((r / RPW) % CPR) (RPW rows per 256-byte bank window, CPR
 // chunks per row); each DMA lane fetches the logical chunk that belongs in
 // its slot. Requires K % BK == 0.
-template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_>
+//
+// XA = 1 gives A one slot more than W (an asymmetric ring, only with S = 2:
+// A 3 slots refilled 3 K-steps ahead, W 2 slots refilled 2 ahead), for
+// GEMMs whose A streams from HBM (see launch_gemm).
+template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_, int XA_ = 0>
 struct DCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, S = STAGES_;
+  static constexpr int XA = XA_, SA = STAGES_ + XA_;
   static constexpr int NW = WM * WN, NT = NW * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -500,12 +505,14 @@ struct DCfg {
   static constexpr int B_INSTR = B_BYTES / 1024 / NW;
   static constexpr int IPS = A_INSTR + B_INSTR;        // per stage per wave
   static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int RING = SA * A_BYTES + S * B_BYTES;  // LDS of the ring
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(A_INSTR * 1024 * NW == A_BYTES && B_INSTR * 1024 * NW == B_BYTES,
                 "every wave issues whole 1 KB DMA blocks");
   static_assert(TM >= 1 && TN >= 1, "wave tile");
   static_assert(S >= 2 && (S - 1) * IPS <= 63, "vmcnt immediate");
-  static_assert(S * STAGE <= 160 * 1024, "LDS");
+  static_assert(RING <= 160 * 1024, "LDS");
+  static_assert(XA == 0 || (XA == 1 && S == 2), "asymmetric ring: A 3 slots, W 2");
 };
 
 // Tiles are walked in groups of `group_m` row-tiles (all column tiles of a
@@ -628,7 +635,7 @@ __device__ __forceinline__ void stage_bf16(const f32x16 (&acc)[C::TM][C::TN],
                                            const f32x4 (&bv)[C::TN][4], uint8_t* smem, int wm,
                                            int wn, int lane, float mul) {
   constexpr int ROWB = C::BN * 2, CPR = ROWB / 16;
-  static_assert(C::BM * ROWB <= C::S * C::STAGE, "staged tile fits the ring");
+  static_assert(C::BM * ROWB <= C::RING, "staged tile fits the ring");
   const int l32 = lane & 31, half = lane >> 5;
   static_for<C::TM>([&](auto i) {
     const int r = wm * C::WTM + i * 32 + l32;
@@ -702,7 +709,7 @@ __device__ __forceinline__ void epi_lds_f32(const EpiParams& e, const f32x16 (&a
                                             const f32x4 (&bv)[C::TN][4], uint8_t* smem, int bm0,
                                             int bn0, int wm, int wn, int lane, int tid) {
   constexpr int ROWB = C::BN * 4, CPR = ROWB / 16;
-  static_assert(C::WTM * ROWB <= C::S * C::STAGE, "staged band fits the ring");
+  static_assert(C::WTM * ROWB <= C::RING, "staged band fits the ring");
   constexpr int PER = C::WTM * CPR / C::NT;
   static_assert(PER * C::NT == C::WTM * CPR, "whole chunks per thread");
   constexpr int BATCH = PER < 8 ? PER : 8;
@@ -766,7 +773,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   // The buffer-resource builtins exist only for the device; the host pass
   // needs nothing but this kernel's launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::S * C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::RING];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -837,6 +844,26 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     n = n < N ? n : N - 1;
     boff[j] = (uint32_t)((int64_t)(n - bn0) * ldw * ES + lchunk * 16);
   }
+  // Asymmetric ring (XA): A slots [SA][A_BYTES] at the start of the ring,
+  // then W slots [S][B_BYTES]; each operand refilled on its own.
+  constexpr bool ASYM = C::XA > 0;
+  uint8_t* const wring = smem + C::SA * C::A_BYTES;
+  auto issue_a = [&](int kt) {
+    uint8_t* base = smem + (kt % C::SA) * C::A_BYTES;
+    const int soff = (kbase + kt * BKE) * ES;
+#pragma unroll
+    for (int j = 0; j < C::A_INSTR; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (lds_ptr_t)(base + (w * C::A_INSTR + j) * 1024), 16, aoff[j], soff, 0, 0);
+  };
+  auto issue_w = [&](int kt) {
+    uint8_t* base = wring + (kt % C::S) * C::B_BYTES;
+    const int soff = (kbase + kt * BKE) * ES;
+#pragma unroll
+    for (int j = 0; j < C::B_INSTR; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rw, (lds_ptr_t)(base + (w * C::B_INSTR + j) * 1024), 16, boff[j], soff, 0, 0);
+  };
   auto issue = [&](int kt) {
     uint8_t* base = smem + (kt % C::S) * C::STAGE;
     const int soff = (kbase + kt * BKE) * ES;
@@ -870,8 +897,9 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   constexpr int NR = C::TM + C::TN, NM = C::TM * C::TN;
   bf16x8 af[2][C::TM], bfr[2][C::TN];
   auto load_frags = [&](int stage, int kk, int set) {
-    const uint8_t* As = smem + (stage % C::S) * C::STAGE;
-    const uint8_t* Bs = As + C::A_BYTES;
+    const uint8_t* As =
+        ASYM ? smem + (stage % C::SA) * C::A_BYTES : smem + (stage % C::S) * C::STAGE;
+    const uint8_t* Bs = ASYM ? wring + (stage % C::S) * C::B_BYTES : As + C::A_BYTES;
     const int slot = ((kk * 2 + half) ^ sw) << 4;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -903,13 +931,34 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   // region, so the reads cannot sink behind the MFMAs and share their
   // registers). The barrier, the refill and the first reads of step kt+1 sit
   // in the last slice, ahead of its MFMAs.
+  // Asymmetric ring: the DMA groups go out in the order A0 W0 A1 W1 A2 in
+  // the prologue, then W(kt+2) A(kt+3) after the barrier of step kt. Step
+  // kt+1's W was issued after step kt-1's barrier and only A(kt+2) after it,
+  // so waiting for step kt+1 leaves A_INSTR in flight: A gets three steps to
+  // land, W two.
+  if constexpr (ASYM) {
+    issue_a(0);
+    issue_w(0);
+    if (nk > 1) {
+      issue_a(1);
+      issue_w(1);
+    }
+    if (nk > 2) issue_a(2);
+    if (nk > 2)
+      wait_vmcnt<2 * C::A_INSTR + C::B_INSTR>();
+    else if (nk > 1)
+      wait_vmcnt<C::A_INSTR + C::B_INSTR>();
+    else
+      wait_vmcnt<0>();
+  } else {
 #pragma unroll
-  for (int st = 0; st < C::S; ++st)
-    if (st < nk) issue(st);
-  if (C::S - 1 < nk)
-    wait_vmcnt<(C::S - 1) * C::IPS>();
-  else
-    wait_vmcnt<0>();
+    for (int st = 0; st < C::S; ++st)
+      if (st < nk) issue(st);
+    if (C::S - 1 < nk)
+      wait_vmcnt<(C::S - 1) * C::IPS>();
+    else
+      wait_vmcnt<0>();
+  }
   __syncthreads();
   load_frags(0, 0, 0);
   // One K-step. ISSUE: refill the slot this step frees with step kt + S;
@@ -946,12 +995,49 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     });
     __builtin_amdgcn_sched_barrier(0);
   };
+  // A step of the asymmetric ring. PH 0 refills W(kt+2) and A(kt+3); 1 only
+  // W(kt+2) (A is complete); 2 nothing; 3 is the last step (no next
+  // fragments). Same ordering of reads, MFMAs and DMA as `step`.
+  auto astep = [&](int kt, auto ph_c) {
+    constexpr int PH = decltype(ph_c)::value;
+    static_for<KS - 1>([&](auto kk) {
+      load_frags(kt, kk + 1, (kk + 1) & 1);
+      mfmas(kk & 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    if (PH <= 1)
+      wait_vmcnt<C::A_INSTR>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's reads done
+    __syncthreads();
+    if (PH <= 2) load_frags(kt + 1, 0, 0);
+    if (PH <= 1) issue_w(kt + 2);
+    if (PH == 0) issue_a(kt + 3);
+    mfmas((KS - 1) & 1);
+    if (PH <= 2) __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+    constexpr int NI = PH == 0 ? C::IPS : PH == 1 ? C::B_INSTR : 0;
+    static_for<NI>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
   using T_ = std::integral_constant<bool, true>;
   using F_ = std::integral_constant<bool, false>;
   int kt = 0;
-  for (; kt + C::S < nk; ++kt) step(kt, T_{}, T_{});
-  for (; kt + 1 < nk; ++kt) step(kt, F_{}, T_{});
-  if (kt < nk) step(kt, F_{}, F_{});
+  if constexpr (ASYM) {
+    for (; kt + 3 < nk; ++kt) astep(kt, std::integral_constant<int, 0>{});
+    for (; kt + 2 < nk; ++kt) astep(kt, std::integral_constant<int, 1>{});
+    for (; kt + 1 < nk; ++kt) astep(kt, std::integral_constant<int, 2>{});
+    if (kt < nk) astep(kt, std::integral_constant<int, 3>{});
+  } else {
+    for (; kt + C::S < nk; ++kt) step(kt, T_{}, T_{});
+    for (; kt + 1 < nk; ++kt) step(kt, F_{}, T_{});
+    if (kt < nk) step(kt, F_{}, F_{});
+  }
 
   if constexpr (I8) {
     // int32 sums -> fp32 (RNE), times the row's and the column's scale, in
@@ -1070,9 +1156,17 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const voi
   // tiles x 8 column tiles for the 128x128 tile, two workgroups per CU) and
   // its L2 loads each A and W strip once. Measured with FETCH_SIZE on the
   // fc1 shape this halves the Infinity Cache / HBM reads (1.41 -> 0.76 GB)
-  // and takes 5 % off the time; for the 256x256 tile (one workgroup per CU)
-  // the plain grouped order measured as good.
-  const int group_m = C::BM == 128 ? 8 : kGroupM, remap = C::BM == 128 ? 1 : 0;
+  // and takes 5 % off the time. For the 256x256 tile (one workgroup per CU)
+  // the same order in groups of 8 row tiles pays only where C is wide: an
+  // XCD's 32 concurrent tiles then span 8 A strips x 4 W strips instead of
+  // 2 x 16 (batch-16 fc1, 20 column tiles: 344 -> 322 us per launch, the
+  // forward 0.5 ms faster in three same-box alternations); with 5 or 15
+  // column tiles (fc2, out-proj, QKV) the plain grouped order measured as
+  // good or better.
+  const int nn_tiles = (N + C::BN - 1) / C::BN;
+  const bool wide = C::BM == 256 && nn_tiles >= 20;
+  const int group_m = C::BM == 128 || wide ? 8 : kGroupM;
+  const int remap = C::BM == 128 || wide ? 1 : 0;
 #define WX_DMA(MD)                                                                   \
   case MD:                                                                           \
     gemm_dma_kernel<C, MD, I8><<<grid, block, 0, s>>>(M, N, K, a, W, ldw, e, group_m, \
@@ -1137,6 +1231,7 @@ static int pick_splits(int M, int N, int K, int64_t tiles, const EpiParams& e) {
 
 using T128 = DCfg<128, 128, 2, 2, 64, 2>;
 using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
+using T256w8a3 = DCfg<256, 256, 2, 4, 64, 2, 1>;  // A three slots (160 KB of LDS)
 using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
 
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
@@ -1154,7 +1249,13 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   // CU) is fastest once there are enough tiles to fill the 256 CUs (batch 16:
   // fc1 367 us vs 399 for 128x128, QKV 269 vs 295, fc2 319 vs 370). Below
   // that (batch 1) the 128x128 tile keeps more CUs busy.
+  // With a long K (batch-16 fc2: K 5120, A = GELU(fc1) 246 MB, too large
+  // to stay in the 256 MB Infinity Cache, so every A stage comes from HBM)
+  // A gets a third slot: three K-steps to land instead of two. fc2 285 vs
+  // 306 us per launch, same bits; the short-K GEMMs (K 1280) gain nothing.
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+  if (big_tiles >= 256 && K >= 3072)
+    return gemm_dma_launch<T256w8a3>(M, N, K, a, W, ldw, mode, e, s);
   if (big_tiles >= 256) return gemm_dma_launch<T256w8>(M, N, K, a, W, ldw, mode, e, s);
   // At most one 128x128 tile per CU (batch 1-2: fc2, out-proj, conv2), the
   // per-step time is the DMA latency: a 3-slot ring (one workgroup per CU)
