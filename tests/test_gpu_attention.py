@@ -37,9 +37,9 @@ def _ref(q, k, v, nh, scale):
 
 @pytest.fixture
 def nosplit(dev):
-    """nosplit(True) makes the device's attention launches use the one-part
-    kernel (WXH_TUNE_ATTN_KEYSPLIT); reset after the test."""
-    yield lambda on: dev.set_tuning(L.WXH_TUNE_ATTN_KEYSPLIT, int(on))
+    """nosplit(mode) sets the device's key split (WXH_TUNE_ATTN_KEYSPLIT):
+    "nosplit" the one-group kernel, else automatic; reset after the test."""
+    yield lambda mode: dev.set_tuning(L.WXH_TUNE_ATTN_KEYSPLIT, int(mode == "nosplit"))
     dev.set_tuning(L.WXH_TUNE_ATTN_KEYSPLIT, 0)
 
 
@@ -57,7 +57,7 @@ def _run(dev, q, k, v, nh, scale, out_dtype=torch.float32):
                                          (1, 1500, 20, "nosplit"), (3, 65, 1, "nosplit")])
 def test_attention_vs_closed_form(dev, B, T, nh, mode, nosplit):
     case(f"attention B={B} T={T} nh={nh} {mode}")
-    nosplit(mode == "nosplit")
+    nosplit(mode)
     rng = np.random.default_rng(T + nh)
     d = nh * 64
     q, k, v = (OB.rb(rng.normal(0, 1, (B, T, d)).astype(np.float32)) for _ in range(3))
@@ -107,7 +107,7 @@ def test_attention_late_max_and_negative_scores(dev, mode, nosplit):
     zero when every score is about -80 (identical keys: O = column mean of V).
     Both against the fp64 closed form."""
     case(f"attention late max / negative scores {mode}")
-    nosplit(mode == "nosplit")
+    nosplit(mode)
     B, T, nh = 1, 1500, 2
     d = nh * 64
     rng = np.random.default_rng(8)

@@ -61,10 +61,10 @@ __device__ __forceinline__ float max_halves(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// KSPLIT = 2 (few workgroups, e.g. batch 1): 8 waves, the first 4 take the
-// first half of the key blocks and the other 4 the second half, for the same
-// 4 x 32 queries, each half through its own ring; the halves' (O, max, sum)
-// are combined through LDS at the end.
+// KSPLIT = 2 (few workgroups, e.g. batch 1): 8 waves, the k-th group of 4
+// takes the k-th share of the key blocks for the same 4 x 32 queries, each
+// group through its own ring; the groups' (O, max, sum) are combined
+// through LDS at the end (written for any KSPLIT).
 template <bool OUT_F32, int KSPLIT, bool QPRE>
 __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -307,32 +307,49 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
                                                       __float_as_uint(l_run), false, false);
     l_run = __uint_as_float(sw2[0]) + __uint_as_float(sw2[1]);
   }
-  if constexpr (KSPLIT == 2) {
-    // The second part hands (O, max, sum) to the first through LDS (idle:
-    // every part's last trip waited for its DMA before the last barrier):
-    // O = O0 2^((m0-m)c) + O1 2^((m1-m)c), l likewise, m = max(m0, m1).
-    float* xs = reinterpret_cast<float*>(smem) + qg * (34 * 64) + lane;
-    if (kh == 1) {
+  if constexpr (KSPLIT > 1) {
+    // Groups 1.. hand (O, max, sum) to group 0 through LDS (idle: every
+    // group's last trip waited for its DMA before the last barrier):
+    // O = sum_k O_k 2^(m_k - m), l likewise, m = max over the groups that
+    // saw keys (a group without key blocks, T <= 64 (KSPLIT - 1), left
+    // l = 0, O = 0 and is skipped).
+    constexpr int kSlot = 34 * 64;  // floats per (group, query group)
+    float* xs = reinterpret_cast<float*>(smem) + lane;
+    if (kh > 0) {
+      float* my = xs + ((kh - 1) * 4 + qg) * kSlot;
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) xs[(db * 16 + r) * 64] = o[db][r];
-      xs[32 * 64] = mc;
-      xs[33 * 64] = l_run;
+        for (int r = 0; r < 16; ++r) my[(db * 16 + r) * 64] = o[db][r];
+      my[32 * 64] = mc;
+      my[33 * 64] = l_run;
     }
     __syncthreads();
-    if (kh == 1) return;
-    // a second part without key blocks (T <= 64) left l = 0, O = 0
-    const float m1 = xs[32 * 64], l1 = xs[33 * 64];
-    const bool has1 = !(l1 == 0.f);
-    const float mm = has1 ? fmaxf(mc, m1) : mc;
+    if (kh > 0) return;
+    float mm = mc, mk[KSPLIT - 1], lk[KSPLIT - 1];
+#pragma unroll
+    for (int k = 0; k < KSPLIT - 1; ++k) {
+      const float* src = xs + (k * 4 + qg) * kSlot;
+      mk[k] = src[32 * 64];
+      lk[k] = src[33 * 64];
+      if (!(lk[k] == 0.f)) mm = fmaxf(mm, mk[k]);
+    }
     const float a0 = __builtin_amdgcn_exp2f(mc - mm);
-    const float a1 = has1 ? __builtin_amdgcn_exp2f(m1 - mm) : 0.f;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * a0 + xs[(db * 16 + r) * 64] * a1;
-    l_run = l_run * a0 + l1 * a1;
+      for (int r = 0; r < 16; ++r) o[db][r] *= a0;
+    l_run *= a0;
+#pragma unroll
+    for (int k = 0; k < KSPLIT - 1; ++k) {
+      const float* src = xs + (k * 4 + qg) * kSlot;
+      const float ak = lk[k] == 0.f ? 0.f : __builtin_amdgcn_exp2f(mk[k] - mm);
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] += src[(db * 16 + r) * 64] * ak;
+      l_run += lk[k] * ak;
+    }
   }
   const float inv = 1.0f / l_run;
   const int q = q0 + l32;
@@ -365,11 +382,14 @@ hipError_t launch_attention(const uint16_t* Q, const uint16_t* K,
   dim3 grid((T + kQB - 1) / kQB, n_head, batch);
   const float scale_log2 = attn_q_scale(scale);
   // Fewer workgroups than CUs (batch 1: 20 heads x 12 query blocks): split
-  // every workgroup's keys over twice the waves, halving each wave's walk.
-  const bool split = (int64_t)grid.x * grid.y * grid.z < 256 && keysplit != 1;
+  // every workgroup's keys over two groups of 4 waves, halving each wave's
+  // walk (-8 % at batch 1; a third group measured no faster). keysplit 1:
+  // never.
+  const bool few = (int64_t)grid.x * grid.y * grid.z < 256;
+  const int ks = !few || keysplit == 1 ? 1 : 2;
   const bool f32 = o_dtype == DT_F32;
 #define WX_ATTN(F32, KS, QP)                                                            \
-  if (f32 == F32 && (KS == 2) == split && q_prescaled == QP)                           \
+  if (f32 == F32 && KS == ks && q_prescaled == QP)                                     \
     attn_kernel<F32, KS, QP><<<grid, 256 * KS, 0, s>>>(Q, K, Vt, n_head, T, Tp, scale_log2, \
                                                        O, ldo);
   WX_ATTN(true, 2, true) WX_ATTN(false, 2, true) WX_ATTN(true, 1, true) WX_ATTN(false, 1, true)

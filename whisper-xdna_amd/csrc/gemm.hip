@@ -486,13 +486,14 @@ using Cfg128 = Cfg<128, 128, 64, 2, 2>;
 // chunks per row); each DMA lane fetches the logical chunk that belongs in
 // its slot. Requires K % BK == 0.
 //
-// XA = 1 gives A one slot more than W (an asymmetric ring, only with S = 2:
-// A 3 slots refilled 3 K-steps ahead, W 2 slots refilled 2 ahead), for
-// GEMMs whose A streams from HBM (see launch_gemm).
-template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_, int XA_ = 0>
+// DEEP = 1 (A) or 2 (W) gives that operand one slot more than the other (an
+// asymmetric ring: S + 1 slots, refilled S + 1 K-steps ahead, against S),
+// for the operand that streams from HBM (see launch_gemm).
+template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_, int DEEP_ = 0>
 struct DCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, S = STAGES_;
-  static constexpr int XA = XA_, SA = STAGES_ + XA_;
+  static constexpr int DEEP = DEEP_;
+  static constexpr int SA = STAGES_ + (DEEP_ == 1), SB = STAGES_ + (DEEP_ == 2);
   static constexpr int NW = WM * WN, NT = NW * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -505,14 +506,14 @@ struct DCfg {
   static constexpr int B_INSTR = B_BYTES / 1024 / NW;
   static constexpr int IPS = A_INSTR + B_INSTR;        // per stage per wave
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int RING = SA * A_BYTES + S * B_BYTES;  // LDS of the ring
+  static constexpr int RING = SA * A_BYTES + SB * B_BYTES;  // LDS of the ring
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(A_INSTR * 1024 * NW == A_BYTES && B_INSTR * 1024 * NW == B_BYTES,
                 "every wave issues whole 1 KB DMA blocks");
   static_assert(TM >= 1 && TN >= 1, "wave tile");
   static_assert(S >= 2 && (S - 1) * IPS <= 63, "vmcnt immediate");
   static_assert(RING <= 160 * 1024, "LDS");
-  static_assert(XA == 0 || (XA == 1 && S == 2), "asymmetric ring: A 3 slots, W 2");
+  static_assert(DEEP >= 0 && DEEP <= 2, "DEEP: 0 none, 1 A, 2 W");
 };
 
 // Tiles are walked in groups of `group_m` row-tiles (all column tiles of a
@@ -844,9 +845,9 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     n = n < N ? n : N - 1;
     boff[j] = (uint32_t)((int64_t)(n - bn0) * ldw * ES + lchunk * 16);
   }
-  // Asymmetric ring (XA): A slots [SA][A_BYTES] at the start of the ring,
-  // then W slots [S][B_BYTES]; each operand refilled on its own.
-  constexpr bool ASYM = C::XA > 0;
+  // Asymmetric ring (DEEP): A slots [SA][A_BYTES] at the start of the ring,
+  // then W slots [SB][B_BYTES]; each operand refilled on its own.
+  constexpr bool ASYM = C::DEEP > 0;
   uint8_t* const wring = smem + C::SA * C::A_BYTES;
   auto issue_a = [&](int kt) {
     uint8_t* base = smem + (kt % C::SA) * C::A_BYTES;
@@ -857,7 +858,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
           ra, (lds_ptr_t)(base + (w * C::A_INSTR + j) * 1024), 16, aoff[j], soff, 0, 0);
   };
   auto issue_w = [&](int kt) {
-    uint8_t* base = wring + (kt % C::S) * C::B_BYTES;
+    uint8_t* base = wring + (kt % C::SB) * C::B_BYTES;
     const int soff = (kbase + kt * BKE) * ES;
 #pragma unroll
     for (int j = 0; j < C::B_INSTR; ++j)
@@ -899,7 +900,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   auto load_frags = [&](int stage, int kk, int set) {
     const uint8_t* As =
         ASYM ? smem + (stage % C::SA) * C::A_BYTES : smem + (stage % C::S) * C::STAGE;
-    const uint8_t* Bs = ASYM ? wring + (stage % C::S) * C::B_BYTES : As + C::A_BYTES;
+    const uint8_t* Bs = ASYM ? wring + (stage % C::SB) * C::B_BYTES : As + C::A_BYTES;
     const int slot = ((kk * 2 + half) ^ sw) << 4;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -931,23 +932,31 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   // region, so the reads cannot sink behind the MFMAs and share their
   // registers). The barrier, the refill and the first reads of step kt+1 sit
   // in the last slice, ahead of its MFMAs.
-  // Asymmetric ring: the DMA groups go out in the order A0 W0 A1 W1 A2 in
-  // the prologue, then W(kt+2) A(kt+3) after the barrier of step kt. Step
-  // kt+1's W was issued after step kt-1's barrier and only A(kt+2) after it,
-  // so waiting for step kt+1 leaves A_INSTR in flight: A gets three steps to
-  // land, W two.
+  // Asymmetric ring, deep operand D (S + 1 slots) and shallow H (S slots).
+  // The DMA groups go out in the order D0 H0 D1 H1 .. D(S-1) H(S-1) D(S) in
+  // the prologue, then H(kt+S) D(kt+S+1) after the barrier of step kt. Step
+  // j's H always follows its D, so waiting for step j means waiting for
+  // H(j): after it come D(j+1) and, in steady state, the S-2 whole steps
+  // issued since, so D_INSTR + (S-2) IPS may stay in flight. D gets S + 1
+  // steps to land, H gets S. Near the end (a refill skipped) the waits are
+  // for everything.
+  constexpr int D_INSTR = C::DEEP == 1 ? C::A_INSTR : C::B_INSTR;
+  auto issue_d = [&](int kt) {
+    if constexpr (C::DEEP == 1) issue_a(kt); else issue_w(kt);
+  };
+  auto issue_h = [&](int kt) {
+    if constexpr (C::DEEP == 1) issue_w(kt); else issue_a(kt);
+  };
   if constexpr (ASYM) {
-    issue_a(0);
-    issue_w(0);
-    if (nk > 1) {
-      issue_a(1);
-      issue_w(1);
-    }
-    if (nk > 2) issue_a(2);
-    if (nk > 2)
-      wait_vmcnt<2 * C::A_INSTR + C::B_INSTR>();
-    else if (nk > 1)
-      wait_vmcnt<C::A_INSTR + C::B_INSTR>();
+    static_for<C::S>([&](auto i) {
+      if (i < nk) {
+        issue_d(i);
+        issue_h(i);
+      }
+    });
+    if (C::S < nk) issue_d(C::S);
+    if (C::S < nk)
+      wait_vmcnt<(C::S - 1) * C::IPS + D_INSTR>();
     else
       wait_vmcnt<0>();
   } else {
@@ -995,11 +1004,12 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     });
     __builtin_amdgcn_sched_barrier(0);
   };
-  // A step of the asymmetric ring. PH 0 refills W(kt+2) and A(kt+3); 1 only
-  // W(kt+2) (A is complete); 2 nothing; 3 is the last step (no next
-  // fragments). Same ordering of reads, MFMAs and DMA as `step`.
-  auto astep = [&](int kt, auto ph_c) {
-    constexpr int PH = decltype(ph_c)::value;
+  // A step of the asymmetric ring. FULL: every refill so far and this
+  // step's, H(kt+S) and D(kt+S+1), exist; otherwise each refill is issued
+  // if its step exists and the wait is for everything. NEXT: read step
+  // kt+1's first fragments. Same ordering of reads, MFMAs and DMA as `step`.
+  auto astep = [&](int kt, auto full_c, auto next_c) {
+    constexpr bool FULL = decltype(full_c)::value, NEXT = decltype(next_c)::value;
     static_for<KS - 1>([&](auto kk) {
       load_frags(kt, kk + 1, (kk + 1) & 1);
       mfmas(kk & 1);
@@ -1007,19 +1017,18 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
       __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
       __builtin_amdgcn_sched_barrier(0);
     });
-    if (PH <= 1)
-      wait_vmcnt<C::A_INSTR>();
+    if (FULL)
+      wait_vmcnt<D_INSTR + (C::S - 2) * C::IPS>();
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's reads done
     __syncthreads();
-    if (PH <= 2) load_frags(kt + 1, 0, 0);
-    if (PH <= 1) issue_w(kt + 2);
-    if (PH == 0) issue_a(kt + 3);
+    if (NEXT) load_frags(kt + 1, 0, 0);
+    if (FULL || kt + C::S < nk) issue_h(kt + C::S);
+    if (FULL || kt + C::S + 1 < nk) issue_d(kt + C::S + 1);
     mfmas((KS - 1) & 1);
-    if (PH <= 2) __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
-    constexpr int NI = PH == 0 ? C::IPS : PH == 1 ? C::B_INSTR : 0;
-    static_for<NI>([&](auto) {
+    if (NEXT) __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+    static_for<FULL ? C::IPS : 0>([&](auto) {
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     });
@@ -1029,10 +1038,9 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   using F_ = std::integral_constant<bool, false>;
   int kt = 0;
   if constexpr (ASYM) {
-    for (; kt + 3 < nk; ++kt) astep(kt, std::integral_constant<int, 0>{});
-    for (; kt + 2 < nk; ++kt) astep(kt, std::integral_constant<int, 1>{});
-    for (; kt + 1 < nk; ++kt) astep(kt, std::integral_constant<int, 2>{});
-    if (kt < nk) astep(kt, std::integral_constant<int, 3>{});
+    for (; kt + C::S + 1 < nk; ++kt) astep(kt, T_{}, T_{});
+    for (; kt + 1 < nk; ++kt) astep(kt, F_{}, T_{});
+    if (kt < nk) astep(kt, F_{}, F_{});
   } else {
     for (; kt + C::S < nk; ++kt) step(kt, T_{}, T_{});
     for (; kt + 1 < nk; ++kt) step(kt, F_{}, T_{});
@@ -1233,6 +1241,7 @@ using T128 = DCfg<128, 128, 2, 2, 64, 2>;
 using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
 using T256w8a3 = DCfg<256, 256, 2, 4, 64, 2, 1>;  // A three slots (160 KB of LDS)
 using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
+using T128w8s3w4 = DCfg<128, 128, 2, 4, 64, 3, 2>;  // W four slots (112 KB)
 
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
                        int64_t ldw, int mode, const EpiParams& e_in,
@@ -1263,8 +1272,12 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   // and split-K adds workgroups where K is long. With more tiles, two
   // workgroups per CU on the 2-slot ring do better (batch 1 QKV 29 vs 37 us).
   const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  // With a long K there (batch-1 fc2, K 5120) W, which streams from HBM
+  // at batch 1 (the model's weights do not fit the Infinity Cache), gets a
+  // fourth slot: fc2 47 -> 44 us per launch, same bits.
   if (tiles128 <= 256) {
     e.splits = pick_splits(M, N, K, tiles128, e);
+    if (K >= 4096) return gemm_dma_launch<T128w8s3w4>(M, N, K, a, W, ldw, mode, e, s);
     return gemm_dma_launch<T128w8s3>(M, N, K, a, W, ldw, mode, e, s);
   }
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, s);
