@@ -175,6 +175,27 @@ def test_hiprt_matmul_plugin(dev):
     np.testing.assert_array_equal(out, out2)
 
 
+@pytest.mark.parametrize("M,N,K", [(1000, 1000, 640), (1500, 1280, 1280)])
+def test_gemm_narrow_tile_epilogues(dev, M, N, K):
+    """At most 128 tiles of 128x128 without a split (the batch-1 out-proj
+    shape, and one with partial edge tiles in both dimensions) run on
+    128x64 tiles: every epilogue against the fp64 product of the same bf16
+    operands, the bf16 ones against RNE / the GELU definitions of the fp32
+    result."""
+    case(f"gemm 128x64 tiles M={M} N={N} K={K}")
+    A, W, b = _operands(M, N, K, seed=M + 7 * N + K)
+    Ad, Wd, bd = _dev(A, dev), _dev(W, dev), _dev(b, dev, False)
+    ref, mag = _exact(A, W, b)
+    acc = dev.gemm(Ad, Wd, bd, L.WXH_EPI_F32).cpu().numpy()
+    assert (np.abs(acc - ref) <= 2e-4 * mag + 1e-6).all()
+    np.testing.assert_array_equal(bits(dev.gemm(Ad, Wd, bd, L.WXH_EPI_BF16)), OB.round_rne(acc))
+    yg = bits(dev.gemm(Ad, Wd, bd, L.WXH_EPI_BF16_GELU_ERF))
+    assert OB.ulp_diff(yg, OB.round_rne(OR.gelu_erf(acc).astype(np.float32))).max() <= 1
+    x0 = np.random.default_rng(M).normal(0, 1, (M, N)).astype(np.float32)
+    x = dev.gemm(Ad, Wd, bd, L.WXH_EPI_RESID_F32, out=_dev(x0, dev, False)).cpu().numpy()
+    np.testing.assert_array_equal(x, (x0 + acc).astype(np.float32))
+
+
 @pytest.mark.parametrize("M,N,K,epi", [(4096 + 100, 4096, 3072, "resid"),
                                        (4096, 4096 + 64, 4096, "bf16"),
                                        (4200, 4096, 3072 + 64, "f32")])

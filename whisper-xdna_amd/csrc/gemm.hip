@@ -1242,6 +1242,7 @@ using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
 using T256w8a3 = DCfg<256, 256, 2, 4, 64, 2, 1>;  // A three slots (160 KB of LDS)
 using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
 using T128w8s3w4 = DCfg<128, 128, 2, 4, 64, 3, 2>;  // W four slots (112 KB)
+using T12864 = DCfg<128, 64, 2, 2, 64, 3>;          // 64x32 per wave, 72 KB
 
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
                        int64_t ldw, int mode, const EpiParams& e_in,
@@ -1277,6 +1278,14 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   // fourth slot: fc2 47 -> 44 us per launch, same bits.
   if (tiles128 <= 256) {
     e.splits = pick_splits(M, N, K, tiles128, e);
+    // Half the CUs or fewer and no split (batch-1 out-proj: K 1280, 120
+    // tiles): 128x64 tiles put twice the workgroups on the CUs, each
+    // streaming 3/4 of the operand bytes per CU that a 128x128 tile does
+    // (the per-CU operand stream bounds these GEMMs): batch-1 out-proj
+    // 15.1 -> 12.7 us run alone, the batch-1 forward 4.72 -> 4.61 ms, same
+    // bits.
+    if (e.splits == 1 && tiles128 <= 128)
+      return gemm_dma_launch<T12864>(M, N, K, a, W, ldw, mode, e, s);
     if (K >= 4096) return gemm_dma_launch<T128w8s3w4>(M, N, K, a, W, ldw, mode, e, s);
     return gemm_dma_launch<T128w8s3>(M, N, K, a, W, ldw, mode, e, s);
   }
