@@ -79,8 +79,9 @@ def _i8_case(rng, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [
-    (100, 200, 128),     # one partial 128x128 tile column/row
-    (1500, 1280, 1280),  # batch-1 out-proj shape: 128x128, 3-slot ring
+    (100, 200, 128),     # partial tiles (128x64, 3-slot ring)
+    (1500, 1280, 1280),  # batch-1 out-proj shape: 120 tiles of 128x128 -> 128x64 tiles
+    (1500, 2560, 1280),  # 240 tiles: 128x128, 8 waves, 3-slot ring
     (1500, 5120, 1280),  # batch-1 fc1 shape: 128x128, 2-slot ring
     (4000, 4096, 256),   # >= 256 tiles of 256x256 (edge rows)
     (6000, 1280, 5120),  # long K

@@ -1307,6 +1307,7 @@ hipError_t launch_gemm_i8(int M, int N, int K, const GemmA& a, const int8_t* W, 
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
   const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
   if (big_tiles >= 256) return gemm_dma_launch<T256w8, true>(M, N, K, a, W, ldw, mode, e, s);
+  if (tiles128 <= 128) return gemm_dma_launch<T12864, true>(M, N, K, a, W, ldw, mode, e, s);
   if (tiles128 <= 256) return gemm_dma_launch<T128w8s3, true>(M, N, K, a, W, ldw, mode, e, s);
   return gemm_dma_launch<T128, true>(M, N, K, a, W, ldw, mode, e, s);
 }
