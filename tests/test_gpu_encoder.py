@@ -123,7 +123,7 @@ def test_large_v3_batch16_bench_workload(dev, large):
     batch of 16 mels of seeds 0..15, one graph replay, where every GEMM runs
     the batch-16 tiles (256x256). Items 0 and 15 against the oracle (the
     large-v3 gate); every item against the same mel run alone at batch 1
-    (128x128 tiles, split-K fc2 and conv2: the same arithmetic up to fp32
+    (128x128 and 128x64 tiles: the same arithmetic up to fp32
     summation order, so far closer to each other than to the oracle); a
     second replay bit for bit."""
     case("encoder large-v3 32 layers batch 16 (bench workload)")
@@ -162,26 +162,27 @@ def test_large_v3_batch16_ctx512(dev, large):
 
 
 def test_split_k_batch1(dev, large):
-    """At batch 1 the large-v3 fc2 (K 5120) and conv2 (K 3840) GEMMs have
-    120 output tiles of 128x128 and split K over two workgroups per tile.
-    The result does not depend on which workgroup of a tile finishes last
+    """Split-K at batch 1. By default the large-v3 GEMMs there run unsplit
+    on 128x64 tiles; forced with the tuning switch, fc2 (K 5120) and conv2
+    (K 3840) split K over two workgroups per 128x128 tile (120 tiles). The
+    split result does not depend on which workgroup of a tile finishes last
     (partials summed in split order): two runs agree bit for bit. It agrees
     with the unsplit GEMMs up to fp32 summation order, and with the oracle."""
     case("encoder large-v3 2 layers batch 1: split-K determinism and parity")
     mel = synth.make_mel(128, 3000, seed=3)
-    a = _fwd(_enc(dev, large, n_layer=2), mel, dev)
-    b = _fwd(_enc(dev, large, n_layer=2), mel, dev)
-    np.testing.assert_array_equal(a, b)
-    dev.set_tuning(L.WXH_TUNE_GEMM_SPLITK, 1)     # encoders made now never split
+    c = _fwd(_enc(dev, large, n_layer=2), mel, dev)
+    dev.set_tuning(L.WXH_TUNE_GEMM_SPLITK, 2)     # encoders made now split 2 ways
     try:
-        c = _fwd(_enc(dev, large, n_layer=2), mel, dev)
+        a = _fwd(_enc(dev, large, n_layer=2), mel, dev)
+        b = _fwd(_enc(dev, large, n_layer=2), mel, dev)
     finally:
         dev.set_tuning(L.WXH_TUNE_GEMM_SPLITK, 0)
+    np.testing.assert_array_equal(a, b)
     ref = OE.encoder_torch(large, mel, n_layer=2)
     c_split, c_plain = cosine(a, ref), cosine(c, ref)
     report("split_k_batch1", cosine_split_vs_plain=cosine(a, c), cosine_split=c_split,
            cosine_plain=c_plain, max_abs_split_vs_plain=float(np.abs(a - c).max()))
-    assert not np.array_equal(a, c), "not splitting should change the summation order"
+    assert not np.array_equal(a, c), "splitting should change the summation order"
     assert cosine(a, c) >= 0.99999
     assert c_split >= 0.9999 and c_plain >= 0.9999
 

@@ -1278,12 +1278,15 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   // fourth slot: fc2 47 -> 44 us per launch, same bits.
   if (tiles128 <= 256) {
     e.splits = pick_splits(M, N, K, tiles128, e);
-    // Half the CUs or fewer and no split (batch-1 out-proj: K 1280, 120
-    // tiles): 128x64 tiles put twice the workgroups on the CUs, each
-    // streaming 3/4 of the operand bytes per CU that a 128x128 tile does
-    // (the per-CU operand stream bounds these GEMMs): batch-1 out-proj
-    // 15.1 -> 12.7 us run alone, the batch-1 forward 4.72 -> 4.61 ms, same
-    // bits.
+    // Half the CUs or fewer: 128x64 tiles put twice the workgroups on the
+    // CUs, each streaming 3/4 of the operand bytes per CU that a 128x128
+    // tile does (the per-CU operand stream bounds these GEMMs). Once that
+    // grid fills three quarters of the CUs it also beats a 2-way split of
+    // the 128x128 tiles, whose fp32 partials cost more than the split gains
+    // (batch-1 large-v3, 120 tiles: out-proj 15.1 -> 12.7 us run alone, the
+    // forward 4.72 -> 4.61 ms; fc2 and conv2 unsplit: 4.45 -> 4.34 ms in
+    // same-box alternations). A forced split (the tuning switch) stays.
+    if (e.force_splits == 0 && tiles128 <= 128 && 2 * tiles128 >= 192) e.splits = 1;
     if (e.splits == 1 && tiles128 <= 128)
       return gemm_dma_launch<T12864>(M, N, K, a, W, ldw, mode, e, s);
     if (K >= 4096) return gemm_dma_launch<T128w8s3w4>(M, N, K, a, W, ldw, mode, e, s);
