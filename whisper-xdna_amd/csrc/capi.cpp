@@ -749,17 +749,6 @@ void set_splitk(wxh_encoder* E, wx::EpiParams& e) {
   e.force_splits = E->tune_splitk;
 }
 
-// Zero rows 0 and T+1 of every batch item of the padded conv1 output (the
-// conv2 im2col reads them as the zero padding).
-__global__ void zero_pad_rows_kernel(uint16_t* x1, int T, int d) {
-  const int b = blockIdx.x;
-  uint16_t* base = x1 + (int64_t)b * (T + 2) * d;
-  for (int c = threadIdx.x; c < d; c += blockDim.x) {
-    base[c] = 0;
-    base[(int64_t)(T + 1) * d + c] = 0;
-  }
-}
-
 struct StageTimer {
   std::vector<std::pair<int, hipEvent_t>> marks;
   hipEvent_t start = nullptr;
@@ -1000,9 +989,8 @@ int forward_impl(wxh_encoder* E, const float* mel, int batch, int frames, float*
   if (E->i8) {
     WXH_HIP(wx::launch_transpose_f32(mel, batch, D.n_mels, frames, E->f32ws, s));
   } else {
-    WXH_HIP(wx::launch_prep_mel(mel, batch, D.n_mels, frames, E->melT, s));
-    zero_pad_rows_kernel<<<batch, 256, 0, s>>>(E->x1, frames, D.d_model);
-    WXH_HIP(hipGetLastError());
+    // also zeroes the pad rows of the conv1 output, which conv2 reads
+    WXH_HIP(wx::launch_prep_mel(mel, batch, D.n_mels, frames, E->melT, s, E->x1, D.d_model));
   }
   if (timer) {
     hipEvent_t ev;

@@ -207,7 +207,10 @@ hipError_t logmel_noalloc_setup(int device);
 hipError_t launch_log_mel_noalloc(int device, const float* audio, int batch, int n_samples,
                                   int n_mels, float* out, hipStream_t s);
 
+// mel [B, C, T] fp32 -> out [B, T + 2, C] bf16 with zero rows 0 and T + 1;
+// with x1 (the conv1 output [B, T + 2, d]) also zeroes x1's rows 0 and
+// T + 1, which conv2's windows read as padding
 hipError_t launch_prep_mel(const float* mel, int batch, int C, int T,
-                           uint16_t* out, hipStream_t s);
+                           uint16_t* out, hipStream_t s, uint16_t* x1 = nullptr, int d = 0);
 
 }  // namespace wx

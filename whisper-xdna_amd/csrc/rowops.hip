@@ -822,7 +822,8 @@ hipError_t launch_convert(const float* x, int64_t ldx, uint16_t* y,
 
 // mel [B, C, T] fp32 -> [B, T + 2, C] bf16 with zero edge rows.
 __global__ __launch_bounds__(256) void prep_mel_kernel(
-    const float* __restrict__ mel, int C, int T, uint16_t* __restrict__ out) {
+    const float* __restrict__ mel, int C, int T, uint16_t* __restrict__ out,
+    uint16_t* __restrict__ x1, int d) {
   __shared__ float tile[64][65];
   const int b = blockIdx.z;
   const int t0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
@@ -844,12 +845,20 @@ __global__ __launch_bounds__(256) void prep_mel_kernel(
       o[(int64_t)(T + 1) * C + c] = 0;
     }
   }
+  // the conv1 output's pad rows (one launch less on the forward's path)
+  if (x1 != nullptr && blockIdx.x == 1 % gridDim.x && blockIdx.y == 0) {
+    uint16_t* xb = x1 + (int64_t)b * (T + 2) * d;
+    for (int c = threadIdx.x; c < d; c += 256) {
+      xb[c] = 0;
+      xb[(int64_t)(T + 1) * d + c] = 0;
+    }
+  }
 }
 
 hipError_t launch_prep_mel(const float* mel, int batch, int C, int T,
-                           uint16_t* out, hipStream_t s) {
+                           uint16_t* out, hipStream_t s, uint16_t* x1, int d) {
   dim3 grid((T + 63) / 64, (C + 63) / 64, batch);
-  prep_mel_kernel<<<grid, 256, 0, s>>>(mel, C, T, out);
+  prep_mel_kernel<<<grid, 256, 0, s>>>(mel, C, T, out, x1, d);
   return hipGetLastError();
 }
 
