@@ -175,13 +175,15 @@ def test_hiprt_matmul_plugin(dev):
     np.testing.assert_array_equal(out, out2)
 
 
-@pytest.mark.parametrize("M,N,K", [(1000, 1000, 640), (1500, 1280, 1280)])
+@pytest.mark.parametrize("M,N,K", [(1000, 1000, 640), (1500, 1280, 1280),
+                                   (1500, 3840, 1280), (1400, 3000, 640)])
 def test_gemm_narrow_tile_epilogues(dev, M, N, K):
-    """At most 128 tiles of 128x128 without a split (the batch-1 out-proj
-    shape, and one with partial edge tiles in both dimensions) run on
-    128x64 tiles: every epilogue against the fp64 product of the same bf16
-    operands, the bf16 ones against RNE / the GELU definitions of the fp32
-    result."""
+    """The batch-1 tile shapes besides 128x128: at most 128 tiles of 128x128
+    without a split run on 128x64 tiles (the out-proj shape, and one with
+    partial edge tiles in both dimensions), 257-512 tiles that fit 256
+    tiles of 128x192 on those (the QKV shape, and one with partial tiles):
+    every epilogue against the fp64 product of the same bf16 operands, the
+    bf16 ones against RNE / the GELU definitions of the fp32 result."""
     case(f"gemm 128x64 tiles M={M} N={N} K={K}")
     A, W, b = _operands(M, N, K, seed=M + 7 * N + K)
     Ad, Wd, bd = _dev(A, dev), _dev(W, dev), _dev(b, dev, False)

@@ -1127,21 +1127,24 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   }
   // Staged epilogues (conditions uniform over the workgroup; the ring is
   // idle once every wave is past the main loop's last barrier: DMA drained,
-  // fragment reads done).
-  if (bm0 + C::BM <= M && bn0 + C::BN <= N) {
-    if constexpr (EMODE == EPI_BF16) {
+  // fragment reads done). Their row swizzle needs a power-of-two number of
+  // 16-byte chunks per row, i.e. BN a power of two; other tiles store
+  // directly.
+  constexpr bool kStaged = (C::BN & (C::BN - 1)) == 0;
+  if (kStaged && bm0 + C::BM <= M && bn0 + C::BN <= N) {
+    if constexpr (kStaged && EMODE == EPI_BF16) {
       if ((e.ldo & 7) == 0 && ((uintptr_t)e.out & 15) == 0) {
         epi_lds_bf16<C>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
         return;
       }
     }
-    if constexpr (EMODE == EPI_QKV) {
+    if constexpr (kStaged && EMODE == EPI_QKV) {
       if (bn0 < 2 * e.d_model && e.d_model % C::BN == 0) {
         epi_lds_qk<C>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
         return;
       }
     }
-    if constexpr (EMODE == EPI_F32 || EMODE == EPI_RESID) {
+    if constexpr (kStaged && (EMODE == EPI_F32 || EMODE == EPI_RESID)) {
       if ((e.ldo & 3) == 0 && ((uintptr_t)e.out & 15) == 0) {
         epi_lds_f32<C, EMODE>(e, acc, bv, smem, bm0, bn0, wm, wn, lane, tid);
         return;
@@ -1243,6 +1246,7 @@ using T256w8a3 = DCfg<256, 256, 2, 4, 64, 2, 1>;  // A three slots (160 KB of LD
 using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
 using T128w8s3w4 = DCfg<128, 128, 2, 4, 64, 3, 2>;  // W four slots (112 KB)
 using T12864 = DCfg<128, 64, 2, 2, 64, 3>;          // 64x32 per wave, 72 KB
+using T128x192 = DCfg<128, 192, 2, 2, 64, 3>;       // 64x96 per wave, 120 KB
 
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
                        int64_t ldw, int mode, const EpiParams& e_in,
@@ -1292,6 +1296,12 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
     if (K >= 4096) return gemm_dma_launch<T128w8s3w4>(M, N, K, a, W, ldw, mode, e, s);
     return gemm_dma_launch<T128w8s3>(M, N, K, a, W, ldw, mode, e, s);
   }
+  // 257-512 tiles of 128x128 leave some CUs with two workgroups and the
+  // rest with one; where 128x192 tiles come to at most 256 (batch-1 QKV:
+  // 360 -> 240) every CU gets one (batch-1 forward 4.34 -> 4.30 ms, same
+  // bits; the 192-wide tile stores its epilogue directly)
+  const int64_t t192 = (int64_t)((M + 127) / 128) * ((N + 191) / 192);
+  if (t192 <= 256) return gemm_dma_launch<T128x192>(M, N, K, a, W, ldw, mode, e, s);
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, s);
 }
 
