@@ -175,15 +175,18 @@ def test_hiprt_matmul_plugin(dev):
     np.testing.assert_array_equal(out, out2)
 
 
-@pytest.mark.parametrize("M,N,K", [(1000, 1000, 640), (1500, 1280, 1280),
-                                   (1500, 3840, 1280), (1400, 3000, 640)])
+@pytest.mark.parametrize("M,N,K", [(1000, 1000, 640), (1000, 1000, 704), (1500, 1280, 1280),
+                                   (1500, 3840, 1280), (1400, 3000, 640), (1500, 5120, 1280)])
 def test_gemm_narrow_tile_epilogues(dev, M, N, K):
     """The batch-1 tile shapes besides 128x128: at most 128 tiles of 128x128
     without a split run on 128x64 tiles (the out-proj shape, and one with
-    partial edge tiles in both dimensions), 257-512 tiles that fit 256
-    tiles of 128x192 on those (the QKV shape, and one with partial tiles):
-    every epilogue against the fp64 product of the same bf16 operands, the
-    bf16 ones against RNE / the GELU definitions of the fp32 result."""
+    partial edge tiles in both dimensions), with K-steps of 128 where K
+    allows and of 64 otherwise (K = 704); 257-512 tiles that fit 256 tiles
+    of 128x192 on those (the QKV shape, and one with partial tiles). The
+    batch-1 shapes also take the XCD block order (the fc1 shape: 480 tiles
+    of 128x128 in 2 x 4 blocks). Every epilogue against the fp64 product of
+    the same bf16 operands, the bf16 ones against RNE / the GELU definitions
+    of the fp32 result."""
     case(f"gemm 128x64 tiles M={M} N={N} K={K}")
     A, W, b = _operands(M, N, K, seed=M + 7 * N + K)
     Ad, Wd, bd = _dev(A, dev), _dev(W, dev), _dev(b, dev, False)

@@ -507,7 +507,7 @@ struct DCfg {
   static constexpr int IPS = A_INSTR + B_INSTR;        // per stage per wave
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int RING = SA * A_BYTES + SB * B_BYTES;  // LDS of the ring
-  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(BK == 32 || BK == 64 || BK == 128, "BK");
   static_assert(A_INSTR * 1024 * NW == A_BYTES && B_INSTR * 1024 * NW == B_BYTES,
                 "every wave issues whole 1 KB DMA blocks");
   static_assert(TM >= 1 && TN >= 1, "wave tile");
@@ -521,7 +521,14 @@ struct DCfg {
 // W columns in L2 / the Infinity Cache. xcd_remap renumbers tile ids so that
 // the ids one XCD receives (every 8th, round-robin dispatch) are a
 // contiguous run of that order.
+// Where the whole grid is resident at once (at most two workgroups per CU)
+// and the tile grid splits evenly, `remap` kXcdBlocks instead hands XCD x
+// (blockIdx % 8) block (x / pc, x % pc) of a pr x pc partition of the tile
+// grid (pr = group_m, pc = 8 / pr): each XCD's L2 then holds the A rows and
+// W columns of one compact block, the partition chosen for the fewest
+// operand bytes per XCD.
 constexpr int kGroupM = 16;
+constexpr int kXcdBlocks = 2;
 
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4],
 // lgkmcnt[11:8]; the other two counters left at their maximum, i.e. not
@@ -796,11 +803,20 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
   const int tile_id = splits > 1 ? gid - split * ntiles : gid;
   const int ksplit = K / splits, kbase = split * ksplit;
   const int pid = tile_id;
-  const int width = group_m * nn;
-  const int first_m = (pid / width) * group_m;
-  const int gsz = min(nm - first_m, group_m);
-  const int tm = first_m + (pid % width) % gsz;
-  const int tn = (pid % width) / gsz;
+  int tm, tn;
+  if (remap == kXcdBlocks) {
+    const int pr = group_m, pc = kXcds / pr;
+    const int bmr = nm / pr, bnc = nn / pc;  // tiles per block: bmr x bnc
+    const int x = blockIdx.x % kXcds, i = blockIdx.x / kXcds;
+    tm = (x / pc) * bmr + i % bmr;
+    tn = (x % pc) * bnc + i / bmr;
+  } else {
+    const int width = group_m * nn;
+    const int first_m = (pid / width) * group_m;
+    const int gsz = min(nm - first_m, group_m);
+    tm = first_m + (pid % width) % gsz;
+    tn = (pid % width) / gsz;
+  }
   const int bm0 = tm * C::BM, bn0 = tn * C::BN;
 
   constexpr int ES = I8 ? 1 : 2;            // bytes per element
@@ -1176,8 +1192,25 @@ static hipError_t gemm_dma_launch(int M, int N, int K, const GemmA& a, const voi
   // good or better.
   const int nn_tiles = (N + C::BN - 1) / C::BN;
   const bool wide = C::BM == 256 && nn_tiles >= 20;
-  const int group_m = C::BM == 128 || wide ? 8 : kGroupM;
-  const int remap = C::BM == 128 || wide ? 1 : 0;
+  int group_m = C::BM == 128 || wide ? 8 : kGroupM;
+  int remap = C::BM == 128 || wide ? 1 : 0;
+  // Block partition over the XCDs (batch 1: at most two 128-row tiles per CU
+  // and no split): the partition with the fewest A rows + W rows per block.
+  // Batch-1 large-v3 fc2 on 128x64 tiles: 4 x 2 blocks of 3 x 10 tiles
+  // (3 A strips and 10 W strips per XCD) instead of runs of 30 tiles of the
+  // grouped order (8 A strips and 4 W strips); the forward 4.50 -> 4.45 ms
+  // in same-box alternations, same bits.
+  if (C::BM == 128 && e.splits == 1 && tiles <= 2 * 256 && tiles % kXcds == 0) {
+    const int nm_tiles = (M + C::BM - 1) / C::BM;
+    int best = 0, best_rows = 0;
+    for (int pr = 1; pr <= kXcds; pr *= 2) {
+      const int pc = kXcds / pr;
+      if (nm_tiles % pr || nn_tiles % pc) continue;
+      const int rows = (nm_tiles / pr) * C::BM + (nn_tiles / pc) * C::BN;
+      if (!best || rows < best_rows) best = pr, best_rows = rows;
+    }
+    if (best) group_m = best, remap = kXcdBlocks;
+  }
 #define WX_DMA(MD)                                                                   \
   case MD:                                                                           \
     gemm_dma_kernel<C, MD, I8><<<grid, block, 0, s>>>(M, N, K, a, W, ldw, e, group_m, \
@@ -1245,7 +1278,8 @@ using T256w8 = DCfg<256, 256, 2, 4, 64, 2>;
 using T256w8a3 = DCfg<256, 256, 2, 4, 64, 2, 1>;  // A three slots (160 KB of LDS)
 using T128w8s3 = DCfg<128, 128, 2, 4, 64, 3>;
 using T128w8s3w4 = DCfg<128, 128, 2, 4, 64, 3, 2>;  // W four slots (112 KB)
-using T12864 = DCfg<128, 64, 2, 2, 64, 3>;          // 64x32 per wave, 72 KB
+using T12864 = DCfg<128, 64, 2, 2, 128, 3>;         // 64x32 per wave, BK 128, 144 KB
+using T12864s = DCfg<128, 64, 2, 2, 64, 3>;         // the same for K % 128 == 64, 72 KB
 using T128x192 = DCfg<128, 192, 2, 2, 64, 3>;       // 64x96 per wave, 120 KB
 
 hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
@@ -1291,8 +1325,15 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
     // forward 4.72 -> 4.61 ms; fc2 and conv2 unsplit: 4.45 -> 4.34 ms in
     // same-box alternations). A forced split (the tuning switch) stays.
     if (e.force_splits == 0 && tiles128 <= 128 && 2 * tiles128 >= 192) e.splits = 1;
-    if (e.splits == 1 && tiles128 <= 128)
+    // The 128x64 tile takes K-steps of 128 (256-byte rows) where K allows:
+    // with two steps in flight that is twice the bytes under way per CU, and
+    // half the barriers, for the weights that stream from HBM at batch 1
+    // (batch-1 forward 4.31 -> 4.21 ms in same-box alternations, same bits;
+    // five 64-wide slots, the same bytes in flight, gave 4.27 ms)
+    if (e.splits == 1 && tiles128 <= 128 && K % 128 == 0)
       return gemm_dma_launch<T12864>(M, N, K, a, W, ldw, mode, e, s);
+    if (e.splits == 1 && tiles128 <= 128)
+      return gemm_dma_launch<T12864s>(M, N, K, a, W, ldw, mode, e, s);
     if (K >= 4096) return gemm_dma_launch<T128w8s3w4>(M, N, K, a, W, ldw, mode, e, s);
     return gemm_dma_launch<T128w8s3>(M, N, K, a, W, ldw, mode, e, s);
   }
@@ -1305,9 +1346,9 @@ hipError_t launch_gemm(int M, int N, int K, const GemmA& a, const uint16_t* W,
   return gemm_dma_launch<T128>(M, N, K, a, W, ldw, mode, e, s);
 }
 
-// Same tile choice as launch_gemm (the K-step covers 128 int8 elements, the
-// bytes of a bf16 step); no split-K, whose fp32 partial sums would not be
-// the exact integer sum.
+// Same tile choice as launch_gemm (a K-step covers twice the int8 elements
+// of a bf16 step, the same bytes); no split-K, whose fp32 partial sums would
+// not be the exact integer sum.
 hipError_t launch_gemm_i8(int M, int N, int K, const GemmA& a, const int8_t* W, int64_t ldw,
                           int mode, const EpiParams& e_in, hipStream_t s) {
   if (M <= 0 || N <= 0) return hipSuccess;
@@ -1320,7 +1361,11 @@ hipError_t launch_gemm_i8(int M, int N, int K, const GemmA& a, const int8_t* W, 
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
   const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
   if (big_tiles >= 256) return gemm_dma_launch<T256w8, true>(M, N, K, a, W, ldw, mode, e, s);
-  if (tiles128 <= 128) return gemm_dma_launch<T12864, true>(M, N, K, a, W, ldw, mode, e, s);
+  // K-steps of 256 int8 elements on the 128x64 tile where K allows (int8
+  // batch-1 forward 4.08 -> 4.00 ms)
+  if (tiles128 <= 128 && K % 256 == 0)
+    return gemm_dma_launch<T12864, true>(M, N, K, a, W, ldw, mode, e, s);
+  if (tiles128 <= 128) return gemm_dma_launch<T12864s, true>(M, N, K, a, W, ldw, mode, e, s);
   if (tiles128 <= 256) return gemm_dma_launch<T128w8s3, true>(M, N, K, a, W, ldw, mode, e, s);
   return gemm_dma_launch<T128, true>(M, N, K, a, W, ldw, mode, e, s);
 }
