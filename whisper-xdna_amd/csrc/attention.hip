@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
     wait_vm<(kStages - 1) * 4>();
   else
     wait_vm<0>();
-  __syncthreads();
+  dma_ring_barrier();
 
   // One 64-key block. The ring slot is a compile-time constant (the loop
   // below is unrolled by kStages), so every LDS read address is a per-lane
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
   auto block = [&](int i, auto slot_c) {
     if (i >= nkb) {  // this part has run out of blocks: keep the barrier count
       wait_vm<0>();
-      __syncthreads();
+      dma_ring_barrier();
       return;
     }
     const int kb = kbeg + i;
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void attn_kernel(
       wait_vm<(kStages - 2) * 4>();
     else
       wait_vm<0>();
-    __syncthreads();
+    dma_ring_barrier();
     if (i + kStages < nkb) issue(i + kStages);
   };
   static_assert(kStages == 3, "the unrolled loop below walks 3 slots");

@@ -93,6 +93,19 @@ __device__ __forceinline__ float wave_max(float v) {
 // blocks of one head) then share an L2.
 constexpr int kXcds = 8;
 
+// Workgroup barrier for the DMA-ring loops (GEMM, attention), whose LDS
+// traffic is direct-to-LDS loads, which each wave has already waited for as
+// far as it needs with an explicit vmcnt, and ds_reads: the wave's reads are
+// waited for here (lgkmcnt(0): no wave may refill a slot another is still
+// reading), then s_barrier, as one asm statement with a memory clobber so
+// the compiler moves no memory access across it. __syncthreads() adds a
+// workgroup-scope fence, for which the compiler first waits for every
+// outstanding LDS DMA of the wave: in a prologue that drains the whole ring,
+// so the first step would wait for the last prologue stage to land.
+__device__ __forceinline__ void dma_ring_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ int xcd_remap(int pid, int total) {
   const int per = (total + kXcds - 1) / kXcds;
   int tall = total % kXcds;

@@ -984,7 +984,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     else
       wait_vmcnt<0>();
   }
-  __syncthreads();
+  dma_ring_barrier();
   load_frags(0, 0, 0);
   // One K-step. ISSUE: refill the slot this step frees with step kt + S;
   // NEXT: read step kt+1's first fragments. Both are compile-time, so each
@@ -1009,7 +1009,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's reads done
-    __syncthreads();
+    dma_ring_barrier();
     if (NEXT) load_frags(kt + 1, 0, 0);
     if (ISSUE) issue(kt + C::S);
     mfmas((KS - 1) & 1);
@@ -1038,7 +1038,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(int M, int N, int K, Ge
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's reads done
-    __syncthreads();
+    dma_ring_barrier();
     if (NEXT) load_frags(kt + 1, 0, 0);
     if (FULL || kt + C::S < nk) issue_h(kt + C::S);
     if (FULL || kt + C::S + 1 < nk) issue_d(kt + C::S + 1);
