@@ -55,7 +55,7 @@ PEAK_I8 = 5.0e15        # MI355X dense int8 MFMA, OP/s
 # what it reads for a 512 MiB device copy (FETCH_SIZE x 2.000, WRITE_SIZE
 # x 1.000); the summaries, with their commands, are in profiles/.
 TRAFFIC_BYTES = {
-    "fc1": (8.123e8, "profiles/gemm_fc1_l16_traffic.md"),
+    "fc1": (8.125e8, "profiles/gemm_fc1_l16_traffic.md"),
     "attention": (2.504e8, "profiles/attention_l16_traffic.md"),
 }
 LARGE = dict(n_mels=128, d=1280, n_head=20, n_layer=32, n_ctx=1500)
