@@ -18,7 +18,8 @@ ROOT = PKG.parent
 CSRC = ROOT / "csrc"
 BUILD = ROOT / "_build"
 LIB = PKG / "libwxhip.so"
-SOURCES = ["rowops.hip", "gemm.hip", "attention.hip", "audio.hip", "quant.hip", "capi.cpp"]
+SOURCES = ["gemm_t256.hip", "gemm_t128.hip", "gemm_t128w8.hip", "gemm_t12864.hip", "gemm.hip",
+           "rowops.hip", "attention.hip", "audio.hip", "quant.hip", "capi.cpp"]
 ARCH = "gfx950"
 # Per-file code generation options. The attention kernel feeds every MFMA
 # result straight into VALU work (softmax, rescaling), and the GEMM
@@ -27,7 +28,9 @@ ARCH = "gfx950"
 # v_accvgpr_read/write copies (about 190 VALU slots per 64-key attention
 # block).
 _VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
-FILE_FLAGS = {"attention.hip": _VGPR_MFMA, "gemm.hip": _VGPR_MFMA}
+FILE_FLAGS = {"attention.hip": _VGPR_MFMA, "gemm.hip": _VGPR_MFMA, "gemm_t256.hip": _VGPR_MFMA,
+              "gemm_t128.hip": _VGPR_MFMA, "gemm_t128w8.hip": _VGPR_MFMA,
+              "gemm_t12864.hip": _VGPR_MFMA}
 
 
 def hipcc():
