@@ -176,12 +176,15 @@ def test_hiprt_matmul_plugin(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(1000, 1000, 640), (1000, 1000, 704), (1500, 1280, 1280),
-                                   (1500, 3840, 1280), (1400, 3000, 640), (1500, 5120, 1280)])
+                                   (1500, 3840, 1280), (1400, 3000, 640), (1500, 5120, 1280),
+                                   (1000, 1000, 128), (1000, 1000, 256), (1000, 1000, 384)])
 def test_gemm_narrow_tile_epilogues(dev, M, N, K):
     """The batch-1 tile shapes besides 128x128: at most 128 tiles of 128x128
     without a split run on 128x64 tiles (the out-proj shape, and one with
     partial edge tiles in both dimensions), with K-steps of 128 where K
-    allows and of 64 otherwise (K = 704); 257-512 tiles that fit 256 tiles
+    allows and of 64 otherwise (K = 704), and with fewer K-steps than ring
+    slots (K = 128, 256: the prologue issues what exists and waits for all
+    of it) or exactly as many (K = 384); 257-512 tiles that fit 256 tiles
     of 128x192 on those (the QKV shape, and one with partial tiles). The
     batch-1 shapes also take the XCD block order (the fc1 shape: 480 tiles
     of 128x128 in 2 x 4 blocks). Every epilogue against the fp64 product of

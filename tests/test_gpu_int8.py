@@ -82,6 +82,8 @@ def _i8_case(rng, M, N, K):
     (100, 200, 128),     # partial tiles (128x64, 3-slot ring)
     (1500, 1280, 1280),  # batch-1 out-proj shape: 120 tiles of 128x128 -> 128x64 tiles
     (1000, 1000, 1152),  # 128x64 tiles with 128-element K-steps (K % 256 != 0)
+    (1000, 1000, 256),   # 256-element K-steps: one step, fewer than the ring's slots
+    (1000, 1000, 512),   # two steps
     (1500, 2560, 1280),  # 240 tiles: 128x128, 8 waves, 3-slot ring
     (1500, 5120, 1280),  # batch-1 fc1 shape: 128x128, 2-slot ring
     (4000, 4096, 256),   # >= 256 tiles of 256x256 (edge rows)
