@@ -4,8 +4,9 @@
 // one per-tensor scale for weights,
 //   scale = max|x| / 127   (1 when the row is all zero)
 //   q     = rint(x / scale)  (round half to even), as int8.
-// The division is the correctly rounded fp32 one (hipcc's default), so
-// q and scale equal numpy's float32 evaluation bit for bit.
+// The quotient is the correctly rounded fp32 one (quant_quotient: one
+// division per row, a corrected product per element), so q and scale equal
+// numpy's float32 evaluation bit for bit.
 //
 // quantize_rows_kernel: one wave per row, the row in registers (NCH chunks
 // of 8 per lane), loads through a per-row buffer descriptor (slots past the
@@ -24,8 +25,9 @@
 
 namespace wx {
 
-__device__ __forceinline__ uint32_t pack_q4(float a, float b, float c, float d, float s) {
-  auto q = [&](float x) { return (uint32_t)((int)rintf(x / s) & 0xFF); };
+__device__ __forceinline__ uint32_t pack_q4(float a, float b, float c, float d,
+                                            const QuantScale& s) {
+  auto q = [&](float x) { return (uint32_t)((int)rintf(quant_quotient(x, s)) & 0xFF); };
   return q(a) | (q(b) << 8) | (q(c) << 16) | (q(d) << 24);
 }
 
@@ -88,12 +90,13 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   }
   int8_t* qr = q + row * ldq;
   const int npc = cols_pad >> 3;
+  const QuantScale qs = quant_scale(s);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int ch = lane + c * 64;
     if (ch >= npc) continue;
-    const u32x2 o = {pack_q4(v[c][0], v[c][1], v[c][2], v[c][3], s),
-                     pack_q4(v[c][4], v[c][5], v[c][6], v[c][7], s)};
+    const u32x2 o = {pack_q4(v[c][0], v[c][1], v[c][2], v[c][3], qs),
+                     pack_q4(v[c][4], v[c][5], v[c][6], v[c][7], qs)};
     *reinterpret_cast<u32x2*>(qr + ch * 8) = o;
   }
 }
@@ -215,12 +218,13 @@ __global__ __launch_bounds__(256) void im2col_quant_kernel(const float* __restri
   if (lane == 0) scale[row] = s;
   int8_t* qr = q + row * ldq;
   const int npc = (int)(ldq >> 3);
+  const QuantScale qs = quant_scale(s);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int ch = lane + c * 64;
     if (ch >= npc) continue;
-    const u32x2 o = {pack_q4(v[c][0], v[c][1], v[c][2], v[c][3], s),
-                     pack_q4(v[c][4], v[c][5], v[c][6], v[c][7], s)};
+    const u32x2 o = {pack_q4(v[c][0], v[c][1], v[c][2], v[c][3], qs),
+                     pack_q4(v[c][4], v[c][5], v[c][6], v[c][7], qs)};
     *reinterpret_cast<u32x2*>(qr + ch * 8) = o;
   }
 }

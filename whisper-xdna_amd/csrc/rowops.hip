@@ -157,10 +157,12 @@ __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cu
     m = wave_max(m) / 127.0f;
     const float sc = m == 0.f ? 1.0f : m;
     if (lane == 0) ysc[row] = sc;
+    const QuantScale qs = quant_scale(sc);
     auto q4 = [&](const float* a) {
       uint32_t w = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) w |= (uint32_t)((int)rintf(a[j] / sc) & 0xFF) << (8 * j);
+      for (int j = 0; j < 4; ++j)
+        w |= (uint32_t)((int)rintf(quant_quotient(a[j], qs)) & 0xFF) << (8 * j);
       return w;
     };
 #pragma unroll
