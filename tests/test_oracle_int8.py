@@ -104,3 +104,39 @@ def test_encoder_int8_fp32_mode_is_the_fp32_encoder_and_perchan_stays_close():
     q = OQ.encoder_int8(W, mel, mode="perchan")
     c = float((q * ref).sum() / np.linalg.norm(q) / np.linalg.norm(ref))
     assert 0.99 < c < 0.99999, c  # quantisation noise is there, and small
+
+
+def _rn32(fr):
+    """A rational rounded to the nearest binary32 (ties to even)."""
+    from fractions import Fraction
+    a = np.float32(float(fr))
+    cands = [a, np.nextafter(a, np.float32(np.inf)), np.nextafter(a, np.float32(-np.inf))]
+    return min(cands, key=lambda c: (abs(Fraction(float(c)) - fr),
+                                     int(np.float32(c).view(np.uint32)) & 1))
+
+
+def test_quantiser_quotient_is_the_correctly_rounded_division():
+    """The device quantisers (quant_quotient in csrc/common.h) form x / s as
+    q0 = RN(x r), then RN(q0 + RN(x - q0 s) r) with r = RN(1 / s) and both
+    steps as single-rounding FMAs (emulated here in exact rational
+    arithmetic), for s in [2^-100, 2^100]. That must equal numpy's float32
+    x / s, which the oracle's rint(x / s) uses, on quotients next to the
+    half-integers where rint turns, and on random ones; scales across the
+    whole allowed range."""
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    for it in range(3000):
+        m = np.float32(2.0 ** rng.choice([rng.uniform(-20, 20), rng.uniform(-92, -80),
+                                          rng.uniform(80, 92)]) * rng.uniform(1, 2))
+        s = np.float32(m / np.float32(127.0))
+        assert 2.0 ** -100 <= s <= 2.0 ** 100
+        r = np.float32(np.float32(1.0) / s)
+        if it % 2:
+            x = np.float32((int(rng.integers(-127, 127)) + 0.5) * float(s))
+            x = np.float32(x + int(rng.integers(-1, 2)) * np.spacing(x))
+        else:
+            x = np.float32(rng.uniform(-1, 1) * float(m))
+        q0 = np.float32(x * r)
+        e = _rn32(-Fraction(float(q0)) * Fraction(float(s)) + Fraction(float(x)))
+        q1 = _rn32(Fraction(float(e)) * Fraction(float(r)) + Fraction(float(q0)))
+        assert q1 == np.float32(x / s), (x, s, q1, np.float32(x / s))
