@@ -233,3 +233,31 @@ def test_gemm_long_k_asymmetric_ring(dev, M, N, K, epi):
         tol = 2e-4 * mag + 1e-6
     err = np.abs(got - ref)
     assert (err <= tol).all(), f"{int((err > tol).sum())} off, max err {err.max()}"
+
+
+def test_gemm_operand_beyond_2gib(dev):
+    """A spans more than 2 GiB (900000 rows of K = 1280 bf16, 2.3 GB): each
+    tile's buffer descriptor starts at that tile's first row, so the DMA
+    kernel addresses the whole operand with 32-bit offsets. Rows on either
+    side of the 2 GiB byte offset, and the first and last rows, against the
+    fp64 product of the same bf16 operands."""
+    M, N, K = 900_000, 64, 1280
+    case(f"gemm A beyond 2 GiB M={M} N={N} K={K}")
+    g = torch.Generator(device=dev.device).manual_seed(11)
+    A = torch.empty(M, K, dtype=torch.bfloat16, device=dev.device)
+    for r0 in range(0, M, 100_000):  # in slices: no 4.6 GB fp32 temporary
+        r1 = min(M, r0 + 100_000)
+        A[r0:r1] = torch.randn(r1 - r0, K, generator=g, device=dev.device).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g, device=dev.device) * 0.05).to(torch.bfloat16)
+    C = dev.gemm(A, W, None, L.WXH_EPI_F32)
+    edge = (1 << 31) // (K * 2)            # the row holding byte 2^31 of A
+    rows = np.array([0, 1, 255, 256, edge - 257, edge - 1, edge, edge + 1, edge + 256,
+                     M - 257, M - 1])
+    idx = torch.from_numpy(rows).to(dev.device)
+    Ar = A.index_select(0, idx).float().cpu().numpy()
+    Wf = W.float().cpu().numpy()
+    ref, mag = _exact(Ar, Wf)
+    got = C.index_select(0, idx).cpu().numpy()
+    assert (np.abs(got - ref) <= 2e-4 * mag + 1e-6).all()
+    del A, C
+    torch.cuda.empty_cache()
