@@ -30,9 +30,16 @@ namespace wx {
 // current row's reductions, so each wave keeps a row in flight while it
 // computes. gamma and beta (or 1 and 0) sit in LDS, loaded once per
 // workgroup. STREAM puts the non-temporal hint on the row loads and the
-// output stores (standalone calls: nothing reads the rows again soon).
-template <int NCH, bool XF32, bool RESID, bool STREAM>
+// output stores (standalone calls: nothing reads the rows again soon); NTL
+// on the row loads only (see launch_layernorm).
+template <int NCH, bool XF32, bool RESID, bool STREAM, bool NTL = false>
 struct LnRow {
+  // Quad layout: fp32 rows without a residual are loaded as lane-contiguous
+  // 16-byte pieces, chunk slot c holding columns (128c + lane) * 4 .. + 3
+  // and (128c + 64 + lane) * 4 .. + 3, so that one load instruction covers
+  // 1 KB of the row (the 8-column chunks take two half-used 2 KB spans).
+  // Measured on the fp32 [24000, 1280] -> bf16 LayerNorm: 35.5 -> 32.7 us.
+  static constexpr bool QL = XF32 && !RESID;
   u32x4 x[NCH][XF32 ? 2 : 1];
   u32x4 r[NCH][RESID ? 2 : 1];
   // Every chunk slot is loaded through a descriptor that covers exactly the
@@ -46,7 +53,7 @@ struct LnRow {
   __device__ __forceinline__ void load(const void* xp, int64_t ldx, const float* rp,
                                        int64_t ldr, int row, int rows, int lane, int cols4) {
     constexpr int esz = XF32 ? 4 : 2;
-    constexpr int aux = STREAM ? 2 : 0;  // cache-policy bit 1: non-temporal
+    constexpr int aux = STREAM || NTL ? 2 : 0;  // cache-policy bit 1: non-temporal
     const bool in = row < rows;
     row = in ? row : 0;
     const int nx = in ? (XF32 ? cols4 : cols4 >> 1) : 0;
@@ -57,8 +64,9 @@ struct LnRow {
     for (int c = 0; c < NCH; ++c)
 #pragma unroll
       for (int h = 0; h < (XF32 ? 2 : 1); ++h)
-        x[c][h] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + c * 64) * 8 * esz + h * 16,
-                                                        0, aux);
+        x[c][h] = __builtin_amdgcn_raw_buffer_load_b128(
+            rs, QL ? ((2 * c + h) * 64 + lane) * 16 : (lane + c * 64) * 8 * esz + h * 16, 0,
+            aux);
     if (RESID) {
       const int nr = in ? cols4 : 0;
       const auto rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rp + row * ldr),
@@ -77,8 +85,8 @@ struct LnRow {
 // YT: DT_BF16, DT_F32, or DT_I8 (the fp32 result quantised per row:
 // scale = max|y| / 127, or 1 for an all-zero row, q = rint(y / scale); the
 // scale goes to ysc[row])
-template <int NCH, bool XF32, int YT, bool RESID, bool STREAM>
-__device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cur,
+template <int NCH, bool XF32, int YT, bool RESID, bool STREAM, bool NTL>
+__device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM, NTL>& cur,
                                        const float* gb, float* __restrict__ sp, int64_t lds,
                                        float eps, void* __restrict__ yp, int64_t ldy, int row,
                                        int lane, int cols, float* __restrict__ ysc) {
@@ -87,6 +95,12 @@ __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cu
   };
   const int nch = cols >> 3;
   const float inv_n = 1.0f / (float)cols;
+  // v[c][4k .. 4k + 3] are columns col_of(c, k) .. + 3: adjacent halves of
+  // the 8-column chunk lane + 64c, or the quad layout's two runs
+  constexpr bool QL = LnRow<NCH, XF32, RESID, STREAM>::QL;
+  auto col_of = [&](int c, int k) {
+    return QL ? ((2 * c + k) * 64 + lane) * 4 : (lane + c * 64) * 8 + 4 * k;
+  };
   float v[NCH][8];
   float sum = 0.f;
 #pragma unroll
@@ -126,11 +140,14 @@ __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cu
   float sq = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    if (lane + c * 64 < nch) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float dlt = v[c][j] - mean;
-        sq += dlt * dlt;
+    for (int k = 0; k < 2; ++k) {
+      if (col_of(c, k) < cols) {
+#pragma unroll
+        for (int j = 4 * k; j < 4 * k + 4; ++j) {
+          const float dlt = v[c][j] - mean;
+          sq += dlt * dlt;
+        }
       }
     }
   }
@@ -140,19 +157,18 @@ __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cu
     float m = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int ch = lane + c * 64;
-      if (ch >= nch) continue;
-      const int64_t col = (int64_t)ch * 8;
-      const f32x4* g = reinterpret_cast<const f32x4*>(gb + col);
-      const f32x4* bb = reinterpret_cast<const f32x4*>(gb + cols + col);
-      const f32x4 g0 = g[0], g1 = g[1], b0 = bb[0], b1 = bb[1];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[c][j] = (v[c][j] - mean) * rstd * g0[j] + b0[j];
-        v[c][j + 4] = (v[c][j + 4] - mean) * rstd * g1[j] + b1[j];
+      for (int k = 0; k < 2; ++k) {
+        const int col = col_of(c, k);
+        if (col >= cols) continue;
+        const f32x4 g = *reinterpret_cast<const f32x4*>(gb + col);
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(gb + cols + col);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[c][4 * k + j] = (v[c][4 * k + j] - mean) * rstd * g[j] + bb[j];
+          m = fmaxf(m, fabsf(v[c][4 * k + j]));
+        }
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[c][j]));
     }
     m = wave_max(m) / 127.0f;
     const float sc = m == 0.f ? 1.0f : m;
@@ -167,40 +183,51 @@ __device__ __forceinline__ void ln_row(const LnRow<NCH, XF32, RESID, STREAM>& cu
     };
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int ch = lane + c * 64;
-      if (ch >= nch) continue;
-      int8_t* y = static_cast<int8_t*>(yp) + row * ldy + (int64_t)ch * 8;
-      st(u32x2{q4(&v[c][0]), q4(&v[c][4])}, reinterpret_cast<u32x2*>(y));
+      int8_t* y = static_cast<int8_t*>(yp) + row * ldy;
+      if (!QL) {
+        if (col_of(c, 0) < cols)
+          st(u32x2{q4(&v[c][0]), q4(&v[c][4])}, reinterpret_cast<u32x2*>(y + col_of(c, 0)));
+        continue;
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (col_of(c, k) < cols)
+          st(q4(&v[c][4 * k]), reinterpret_cast<uint32_t*>(y + col_of(c, k)));
     }
     return;
   }
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int ch = lane + c * 64;
-    if (ch >= nch) continue;
-    const int64_t col = (int64_t)ch * 8;
-    const f32x4* g = reinterpret_cast<const f32x4*>(gb + col);
-    const f32x4* bb = reinterpret_cast<const f32x4*>(gb + cols + col);
-    const f32x4 g0 = g[0], g1 = g[1], b0 = bb[0], b1 = bb[1];
     float o[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[j] = (v[c][j] - mean) * rstd * g0[j] + b0[j];
-      o[j + 4] = (v[c][j + 4] - mean) * rstd * g1[j] + b1[j];
+    for (int k = 0; k < 2; ++k) {
+      const int col = col_of(c, k) < cols ? col_of(c, k) : 0;
+      const f32x4 g = *reinterpret_cast<const f32x4*>(gb + col);
+      const f32x4 bb = *reinterpret_cast<const f32x4*>(gb + cols + col);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[4 * k + j] = (v[c][4 * k + j] - mean) * rstd * g[j] + bb[j];
     }
     if (YT == DT_F32) {
-      float* y = static_cast<float*>(yp) + row * ldy + col;
-      st(f32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<f32x4*>(y));
-      st(f32x4{o[4], o[5], o[6], o[7]}, reinterpret_cast<f32x4*>(y + 4));
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (col_of(c, k) < cols)
+          st(f32x4{o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]},
+             reinterpret_cast<f32x4*>(static_cast<float*>(yp) + row * ldy + col_of(c, k)));
+    } else if (!QL) {
+      if (col_of(c, 0) < cols)
+        st(u32x4{f2bf2(o[0], o[1]), f2bf2(o[2], o[3]), f2bf2(o[4], o[5]), f2bf2(o[6], o[7])},
+           reinterpret_cast<u32x4*>(static_cast<uint16_t*>(yp) + row * ldy + col_of(c, 0)));
     } else {
-      uint16_t* y = static_cast<uint16_t*>(yp) + row * ldy + col;
-      st(u32x4{f2bf2(o[0], o[1]), f2bf2(o[2], o[3]), f2bf2(o[4], o[5]), f2bf2(o[6], o[7])},
-         reinterpret_cast<u32x4*>(y));
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (col_of(c, k) < cols)
+          st(u32x2{f2bf2(o[4 * k], o[4 * k + 1]), f2bf2(o[4 * k + 2], o[4 * k + 3])},
+             reinterpret_cast<u32x2*>(static_cast<uint16_t*>(yp) + row * ldy + col_of(c, k)));
     }
   }
 }
 
-template <int NCH, bool XF32, int YT, bool RESID, bool STREAM>
+template <int NCH, bool XF32, int YT, bool RESID, bool STREAM, bool NTL = false>
 __global__ __launch_bounds__(256) void ln_kernel(
     const void* __restrict__ xp, int64_t ldx, const float* __restrict__ rp,
     int64_t ldr, float* __restrict__ sp, int64_t lds,
@@ -217,7 +244,7 @@ __global__ __launch_bounds__(256) void ln_kernel(
   // two row buffers in turn (no register copies, which would wait for the
   // loads in flight); the first row's loads go out before gamma and beta
   // are fetched, so the two trips to memory overlap
-  LnRow<NCH, XF32, RESID, STREAM> ra, rb;
+  LnRow<NCH, XF32, RESID, STREAM, NTL> ra, rb;
   int row = row0;
   ra.load(xp, ldx, rp, ldr, row, rows, lane, cols4);
   {
@@ -251,13 +278,13 @@ __global__ __launch_bounds__(256) void ln_kernel(
   __syncthreads();
   while (row < rows) {
     rb.load(xp, ldx, rp, ldr, row + waves, rows, lane, cols4);
-    ln_row<NCH, XF32, YT, RESID, STREAM>(ra, ln_gb, sp, lds, eps, yp, ldy, row, lane, cols,
-                                         ysc);
+    ln_row<NCH, XF32, YT, RESID, STREAM, NTL>(ra, ln_gb, sp, lds, eps, yp, ldy, row, lane,
+                                              cols, ysc);
     row += waves;
     if (row >= rows) break;
     ra.load(xp, ldx, rp, ldr, row + waves, rows, lane, cols4);
-    ln_row<NCH, XF32, YT, RESID, STREAM>(rb, ln_gb, sp, lds, eps, yp, ldy, row, lane, cols,
-                                         ysc);
+    ln_row<NCH, XF32, YT, RESID, STREAM, NTL>(rb, ln_gb, sp, lds, eps, yp, ldy, row, lane,
+                                              cols, ysc);
     row += waves;
   }
 }
@@ -272,19 +299,28 @@ static hipError_t ln_dispatch(const void* x, int x_dtype, int64_t ldx,
                               int64_t lds, const float* gamma,
                               const float* beta, float eps, void* y,
                               int y_dtype, int64_t ldy, int rows, int cols,
-                              bool stream, hipStream_t s, float* ysc) {
+                              bool stream, bool ntl, hipStream_t s, float* ysc) {
   dim3 grid(std::min((rows + 3) / 4, kLnGrid)), block(256);
   const size_t smem = 2 * (size_t)cols * sizeof(float);
   const bool xf = x_dtype == DT_F32, r = resid != nullptr;
   const int yt = y_dtype;
+#define WX_LN_NTL(YT)                                                                  \
+  if (ntl)                                                                             \
+    ln_kernel<NCH, true, YT, false, false, true><<<grid, block, smem, s>>>(            \
+        x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols, ysc);   \
+  else                                                                                 \
+    ln_kernel<NCH, true, YT, false, false, false><<<grid, block, smem, s>>>(           \
+        x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols, ysc);   \
+  return hipGetLastError();
   if (yt == DT_I8) {
     // the int8 encoder's LayerNorm only: fp32 residual stream in, no fused
     // residual add, cached stores
     if (!xf || r || stream) return hipErrorInvalidValue;
-    ln_kernel<NCH, true, DT_I8, false, false><<<grid, block, smem, s>>>(
-        x, ldx, resid, ldr, sum_out, lds, gamma, beta, eps, y, ldy, rows, cols, ysc);
-    return hipGetLastError();
+    WX_LN_NTL(DT_I8)
   }
+  // the encoder's LayerNorm (fp32 residual stream in, cached stores)
+  if (xf && !r && !stream && yt == DT_BF16) { WX_LN_NTL(DT_BF16) }
+#undef WX_LN_NTL
 #define WX_LN(XF, YT, R)                                                             \
   if (xf == XF && yt == YT && r == R) {                                              \
     if (stream)                                                                      \
@@ -310,12 +346,23 @@ hipError_t launch_layernorm(const void* x, int x_dtype, int64_t ldx,
                             int rows, int cols, bool stream, hipStream_t s,
                             float* y_scale) {
   if (rows <= 0) return hipSuccess;
+  // The encoder's LayerNorm (cached stores: the next GEMM reads its output)
+  // loads a large fp32 residual stream with the non-temporal hint, so that
+  // the stream does not push the GEMMs' operands out of L2 and the Infinity
+  // Cache: batch-16 large-v3 forward 38.62 -> 38.45 ms, int8 34.63 ->
+  // 34.34. A small one is still in the Infinity Cache when the residual
+  // GEMM that follows reads it again, and the hint costs that reuse (batch 1:
+  // 4.19 -> 4.26 ms). Between the two reads the stream, the LayerNorm's
+  // output and the QKV and attention outputs come to 3.5 times the stream;
+  // the switch sits at 64 MB, where that is 224 of the cache's 256 MB.
+  const bool ntl = !stream && x_dtype == DT_F32 && !resid &&
+                   (int64_t)rows * cols * 4 >= (int64_t)64 << 20;
   // chunks of 8 per lane: 64 lanes x 8 = 512 columns per chunk
   switch ((cols + 511) / 512) {
 #define WX_LNC(N)                                                                   \
     case N:                                                                         \
       return ln_dispatch<N>(x, x_dtype, ldx, resid, ldr, sum_out, lds, gamma, beta, \
-                            eps, y, y_dtype, ldy, rows, cols, stream, s, y_scale);
+                            eps, y, y_dtype, ldy, rows, cols, stream, ntl, s, y_scale);
     WX_LNC(1) WX_LNC(2) WX_LNC(3) WX_LNC(4) WX_LNC(5) WX_LNC(6) WX_LNC(7) WX_LNC(8)
 #undef WX_LNC
   }
