@@ -55,20 +55,26 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   const auto rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<char*>(static_cast<const char*>(xp) + row * ldx * esz), (short)0, nbytes,
       0x00020000);
+  // fp32 rows are read as lane-contiguous 16-byte pieces: v[c][4k .. 4k + 3]
+  // are columns col_of(c, k) .. + 3, so one load instruction covers 1 KB of
+  // the row (8-column chunks per lane would take two half-used 2 KB spans);
+  // bf16 rows keep 8-column chunks, one 16-byte piece per lane
+  auto col_of = [&](int c, int k) {
+    return XF32 ? ((2 * c + k) * 64 + lane) * 4 : (lane + c * 64) * 8 + 4 * k;
+  };
   float v[NCH][8];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int off = (lane + c * 64) * 8 * esz;
     if (XF32) {
-      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kCpolNt);
-      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, kCpolNt);
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, col_of(c, 0) * 4, 0, kCpolNt);
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rs, col_of(c, 1) * 4, 0, kCpolNt);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         v[c][j] = __uint_as_float(a[j]);
         v[c][j + 4] = __uint_as_float(b[j]);
       }
     } else {
-      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kCpolNt);
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, col_of(c, 0) * 2, 0, kCpolNt);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         v[c][2 * j] = __uint_as_float(w[j] << 16);
@@ -89,15 +95,20 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     if (lane == 0) scale[row] = s;
   }
   int8_t* qr = q + row * ldq;
-  const int npc = cols_pad >> 3;
   const QuantScale qs = quant_scale(s);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int ch = lane + c * 64;
-    if (ch >= npc) continue;
-    const u32x2 o = {pack_q4(v[c][0], v[c][1], v[c][2], v[c][3], qs),
-                     pack_q4(v[c][4], v[c][5], v[c][6], v[c][7], qs)};
-    *reinterpret_cast<u32x2*>(qr + ch * 8) = o;
+    if (XF32) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (col_of(c, k) < cols_pad)
+          *reinterpret_cast<uint32_t*>(qr + col_of(c, k)) =
+              pack_q4(v[c][4 * k], v[c][4 * k + 1], v[c][4 * k + 2], v[c][4 * k + 3], qs);
+    } else if (col_of(c, 0) < cols_pad) {
+      const u32x2 o = {pack_q4(v[c][0], v[c][1], v[c][2], v[c][3], qs),
+                       pack_q4(v[c][4], v[c][5], v[c][6], v[c][7], qs)};
+      *reinterpret_cast<u32x2*>(qr + col_of(c, 0)) = o;
+    }
   }
 }
 
