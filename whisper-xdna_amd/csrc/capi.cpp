@@ -483,10 +483,11 @@ int wxh_attention(wxh_ctx* c, const uint16_t* Q, const uint16_t* K,
 
 namespace {
 
-// The encoder's LayerNorms load and store without the non-temporal hint:
-// the next GEMM reads h straight after, and the residual stream x is read
-// again by the out-projection / fc2 epilogues (with the hint the 64
+// The encoder's LayerNorms store without the non-temporal hint: the next
+// GEMM reads h straight after (with the hint on loads and stores the 64
 // LayerNorms took 2.60 ms per batch-16 forward instead of 2.28).
+// launch_layernorm itself puts the hint on the loads of a residual stream
+// of 64 MB or more.
 constexpr bool kEncLnStream = false;
 
 struct LayerW {

@@ -17,7 +17,9 @@ enum Gelu { GELU_NONE = -1, GELU_ERF = 0, GELU_POLY4_RNE = 1, GELU_POLY4_TRUNC =
 // ---------------------------------------------------------------- row ops
 // y = LN(x [+ resid]) * gamma + beta over each row of `cols` elements.
 // sum_out (fp32, optional) receives x + resid before normalisation.
-// stream: non-temporal loads and stores (for rows nothing reads again soon).
+// stream: non-temporal loads and stores (for rows nothing reads again soon);
+// without it, an fp32 x of 64 MB or more (no resid) still gets non-temporal
+// loads, the output cached stores.
 // y_dtype DT_I8: y is the row quantised per row (launch_quantize_rows'
 // rule, on the fp32 LN output) with its scale in y_scale[row].
 hipError_t launch_layernorm(const void* x, int x_dtype, int64_t ldx,
